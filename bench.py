@@ -1,0 +1,242 @@
+"""Benchmark of the MI355X MoE forward (one GPU).
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload qwen-bf16-t17]
+
+A step is one full router-inclusive MoE layer forward (router -> planner ->
+gate/up+SwiGLU -> down -> combine) over inputs already resident in HBM,
+replayed from a HIP graph.  Two copies of the weights alternate between steps
+so the 256 MB Infinity Cache cannot serve a step from the previous one.  The
+JSON line's ``value`` is tokens/s of ``--workload`` (default: BASELINE
+configs[1], Qwen3-30B-A3B shape, BF16, T=17); ``sweep`` carries every
+BASELINE MoE configuration.  ``roofline`` is the dominant kernel
+(gate/up+SwiGLU) timed live with HIP events on the stream it runs on;
+``cpu_baseline`` times the FP32 CPU oracle on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "MoE layer µs + tokens/s at T=17/193/1024 (BF16, W4A16); % HBM/MFMA roofline"
+
+WORKLOADS = {
+    "qwen-bf16-t17": dict(shape="qwen", T=17, routing="uniform", w4=False),
+    "qwen-bf16-t193": dict(shape="qwen", T=193, routing="uniform", w4=False),
+    "qwen-bf16-t1024-zipf": dict(shape="qwen", T=1024, routing="zipf", w4=False),
+    "qwen-w4-t17": dict(shape="qwen", T=17, routing="uniform", w4=True),
+    "qwen-w4-t193": dict(shape="qwen", T=193, routing="uniform", w4=True),
+    "qwen-w4-t1024": dict(shape="qwen", T=1024, routing="uniform", w4=True),
+    "tiny-bf16-t17": dict(shape="tiny", T=17, routing="uniform", w4=False),
+}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_plans(spec, device, copies=2):
+    """Prepared layers sharing inputs, each with its own weight copy."""
+    from llm_gpu_kernels_amd import prepare_routed_moe, quantize_gate_up, tile_gate_up
+    from llm_gpu_kernels_amd.workloads import make_layer
+    lay = make_layer(spec["shape"], spec["T"], routing=spec["routing"], seed=0, device=device)
+    gate_up = lay["gate_up"]
+    if spec["w4"]:
+        gate_up = tile_gate_up(quantize_gate_up(gate_up.cpu())).to(device)
+    plans = []
+    for c in range(copies):
+        if c == 0:
+            gu, dn = gate_up, lay["down"]
+        elif spec["w4"]:
+            gu = type(gate_up)(gate_up.words.clone(), gate_up.scales.clone(), gate_up.logical_shape)
+            dn = lay["down"].clone()
+        else:
+            gu, dn = gate_up.clone(), lay["down"].clone()
+        plans.append(prepare_routed_moe(lay["x"], lay["logits"], gu, dn, lay["K"]))
+    torch.cuda.synchronize()
+    return lay, plans
+
+
+def algorithmic(spec, lay, plan):
+    """Bytes and FLOPs one forward must move / compute (weights of active experts once)."""
+    e, h, inter, k, t = lay["E"], lay["H"], lay["I"], lay["K"], spec["T"]
+    counts = plan.counts.cpu()
+    active = int((counts > 0).sum())
+    if spec["w4"]:
+        gu_bytes = 2 * inter * h // 2 + 2 * inter * (h // 128) * 2
+    else:
+        gu_bytes = 2 * inter * h * 2
+    dn_bytes = h * inter * 2
+    layer_bytes = active * (gu_bytes + dn_bytes) + t * h * 2 + t * e * 4 + t * h * 2
+    gate_up_bytes = active * gu_bytes + t * h * 2 + t * k * inter * 2
+    flops = 6 * t * k * h * inter + 3 * t * e
+    return dict(active_experts=active, layer_bytes=layer_bytes, gate_up_bytes=gate_up_bytes,
+                flops=flops, gate_up_flops=4 * t * k * h * inter)
+
+
+def time_layer(plans, steps, warmup):
+    """Average ms per forward over `steps` graph replays (alternating weight copies)."""
+    graphs = []
+    stream = torch.cuda.Stream()
+    for p in plans:
+        for _ in range(2):
+            p.run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            p.run()
+        graphs.append(g)
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    # per-step samples for p50/p95
+    samples = []
+    for i in range(min(steps, 40)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graphs[i % len(graphs)].replay()
+        b.record()
+        b.synchronize()
+        samples.append(a.elapsed_time(b))
+    return total_ms / steps, samples
+
+
+def time_stage(plans, stage, reps=40):
+    """Average duration (ms) of one launch of `stage`, HIP events on its stream."""
+    for p in plans:
+        p.run()
+    torch.cuda.synchronize()
+    durations = []
+    for i in range(reps):
+        p = plans[i % len(plans)]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        p.run_stage(stage)
+        b.record()
+        durations.append((a, b))
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in durations)
+
+
+def measure(name, steps, warmup, device):
+    spec = WORKLOADS[name]
+    lay, plans = build_plans(spec, device)
+    alg = algorithmic(spec, lay, plans[0])
+    ms, samples = time_layer(plans, steps, warmup)
+    gate_idx = plans[0].launches.index("gate_up_swiglu")
+    gu_ms = time_stage(plans, gate_idx)
+    stage_ms = {n: round(time_stage(plans, i, reps=20) * 1e3, 2) for i, n in enumerate(plans[0].launches)}
+    t = spec["T"]
+    layer_gbs = alg["layer_bytes"] / (ms * 1e-3) / 1e9
+    tflops = alg["flops"] / (ms * 1e-3) / 1e12
+    attainable = min(BF16_PEAK_TFLOPS, alg["flops"] / alg["layer_bytes"] * HBM_PEAK_GBS / 1e3)
+    res = dict(
+        workload=name, T=t, weights="w4g128+bf16-down" if spec["w4"] else "bf16",
+        routing=spec["routing"], us_per_layer=round(ms * 1e3, 2),
+        p50_us=round(statistics.median(samples) * 1e3, 2),
+        p95_us=round(sorted(samples)[int(0.95 * (len(samples) - 1))] * 1e3, 2),
+        tokens_per_s=round(t / (ms * 1e-3), 1), active_experts=alg["active_experts"],
+        layer_bytes=alg["layer_bytes"], layer_hbm_gbs=round(layer_gbs, 1),
+        layer_hbm_frac=round(layer_gbs / HBM_PEAK_GBS, 4),
+        layer_tflops=round(tflops, 2), mfma_frac=round(tflops / BF16_PEAK_TFLOPS, 4),
+        attainable_roofline_frac=round(tflops / attainable, 4),
+        stage_us=stage_ms,
+        gate_up=dict(us=round(gu_ms * 1e3, 2), bytes=alg["gate_up_bytes"],
+                     gbs=round(alg["gate_up_bytes"] / (gu_ms * 1e-3) / 1e9, 1)),
+    )
+    return res, lay, plans
+
+
+def cpu_baseline(lay, spec, budget_s=12.0):
+    """FP32 CPU oracle (reference.py:17-45 restated) + CPU router, bounded sample."""
+    from oracle.moe_oracle import moe_reference, route_topk
+    x, gu, dn, logits = (lay["x"].cpu(), lay["gate_up"].cpu(), lay["down"].cpu(),
+                         lay["logits"].cpu())
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end and len(times) < 20:
+        t0 = time.perf_counter()
+        ids, w = route_topk(logits, lay["K"])
+        moe_reference(x, gu, dn, ids, w)
+        times.append(time.perf_counter() - t0)
+    mean = statistics.mean(times)
+    return {"value": round(spec["T"] / mean, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "us_per_layer": round(mean * 1e6, 1),
+            "sample": f"{len(times)} full forwards of the {spec['shape']} T={spec['T']} layer "
+                      f"(oracle.moe_oracle.route_topk + moe_reference, FP32, torch CPU, "
+                      f"os.cpu_count()={os.cpu_count()})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="qwen-bf16-t17", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(one MI355X per box); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    log(f"[bench] workload {args.workload}")
+    main_res, lay, plans = measure(args.workload, args.steps, args.warmup, device)
+    spec = WORKLOADS[args.workload]
+    sweep = []
+    if not args.no_sweep:
+        for name in WORKLOADS:
+            if name == args.workload:
+                sweep.append(main_res)
+                continue
+            log(f"[bench] sweep {name}")
+            r, _, p = measure(name, args.steps, args.warmup, device)
+            sweep.append(r)
+            del p
+            torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(lay, spec)
+    gu = main_res["gate_up"]
+    line = {
+        "metric": METRIC, "value": main_res["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(main_res["us_per_layer"] / 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": args.workload, "shape": spec["shape"], "T": spec["T"],
+                   "E": lay["E"], "H": lay["H"], "I": lay["I"], "top_k": lay["K"],
+                   "weights": main_res["weights"], "routing": spec["routing"],
+                   "router": "on-GPU softmax-topk-renorm", "parallelism": "single-gpu"},
+        "us_per_layer": main_res["us_per_layer"],
+        "roofline": {"bound": "hbm", "kernel": "gate_up_swiglu", "achieved": gu["gbs"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "avg_us": gu["us"], "algorithmic_bytes": gu["bytes"]},
+        "layer_roofline": {"bound": "hbm", "achieved": main_res["layer_hbm_gbs"],
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": main_res["layer_hbm_frac"]},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

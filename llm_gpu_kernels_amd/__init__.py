@@ -1,0 +1,18 @@
+"""MI355X-native (gfx950) MoE forward: routing, grouped expert GEMMs, combine.
+
+The Python layer mirrors the reference's prepared operator API; all compute
+runs in hand-written HIP kernels of ``_lib/libmoe_mi355x.so`` (C ABI in
+``include/``).  Importing the package does not load the library; the first
+prepare/quantise call does, and raises if it has not been built.
+"""
+from .moe import (FrozenMoEPolicy, GemmConfig, PreparedMoE, PreparedRoutedMoE, prepare_configured_moe,
+                  prepare_cuda_moe, prepare_moe, prepare_ranked_moe_launcher, prepare_routed_moe,
+                  prepare_w4_layout_moe, prepare_w4_moe)
+from .weight_quant import PackedGateUp, TiledGateUp, dequantize_tiled, quantize_gate_up, tile_gate_up
+
+__all__ = [
+    "FrozenMoEPolicy", "GemmConfig", "PreparedMoE", "PreparedRoutedMoE", "prepare_configured_moe",
+    "prepare_cuda_moe", "prepare_moe", "prepare_ranked_moe_launcher", "prepare_routed_moe",
+    "prepare_w4_layout_moe", "prepare_w4_moe", "PackedGateUp", "TiledGateUp", "dequantize_tiled",
+    "quantize_gate_up", "tile_gate_up",
+]

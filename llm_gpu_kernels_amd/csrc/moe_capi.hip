@@ -1,0 +1,312 @@
+// C ABI for the MI355X MoE forward (include/moe_mi355x.h).
+//
+// Validation mirrors prepare_moe (src/llm_gpu_kernels/moe.py:220-235) and the
+// contract of docs/MOE_USAGE.md:13-34: 1 <= E <= 256, H > 0, I > 0,
+// 1 <= K <= 32, R = T*K < 2^31, R * max(H, 2I) < 2^31.  A plan stores
+// pointers only; the caller owns every buffer.  moe_plan_run enqueues on the
+// given stream with no synchronisation and no allocation.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "../../include/moe_mi355x.h"
+#include "moe_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(MOE_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Router fused into the planner's single workgroup up to this many logits.
+constexpr long long kFuseRouterLogits = 64 * 1024;
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int choose_token_block(const moe_desc *d) {
+  if (d->token_block == 16 || d->token_block == 32) return d->token_block;
+  // Mean rows per expert: small -> 16-row tasks, otherwise 32.
+  const long long r = (long long)d->T * d->K;
+  return r <= 16LL * d->E ? 16 : 32;
+}
+
+bool shape_fast(const moe_desc *d, int tb) {
+  if (d->H % 128 || d->I % 128) return false;
+  if (moe::gate_up_lds_bytes(d->H, tb) > moe::kMaxLds) return false;
+  if (moe::down_lds_bytes(d->I, tb) > moe::kMaxLds) return false;
+  if (d->H > 4096 || d->I > 4096) return false;
+  return true;
+}
+
+int validate(const moe_desc *d) {
+  if (!d) return fail(MOE_EINVAL, "null descriptor");
+  if (d->E < 1 || d->E > 256) return fail(MOE_EINVAL, "E must be in [1, 256] (got %d)", d->E);
+  if (d->H <= 0 || d->I <= 0) return fail(MOE_EINVAL, "H and I must be positive");
+  if (d->K < 1 || d->K > 32) return fail(MOE_EINVAL, "top-k must be in [1, 32] (got %d)", d->K);
+  if (d->T < 0) return fail(MOE_EINVAL, "T must be >= 0");
+  const long long r = (long long)d->T * d->K;
+  const long long wide = d->H > 2LL * d->I ? d->H : 2LL * d->I;
+  if (r >= (1LL << 31) || r * wide >= (1LL << 31))
+    return fail(MOE_EINVAL, "R=T*K and R*max(H,2I) must be < 2^31");
+  if (d->weight_format != MOE_WEIGHTS_BF16 && d->weight_format != MOE_WEIGHTS_W4G128)
+    return fail(MOE_EINVAL, "unknown weight format %d", d->weight_format);
+  if (d->id_dtype != MOE_IDS_INT32 && d->id_dtype != MOE_IDS_INT64)
+    return fail(MOE_EINVAL, "unknown id dtype %d", d->id_dtype);
+  if (d->route_mode != MOE_ROUTE_FIXED && d->route_mode != MOE_ROUTE_LOGITS)
+    return fail(MOE_EINVAL, "unknown route mode %d", d->route_mode);
+  if (d->route_mode == MOE_ROUTE_LOGITS) {
+    if (d->id_dtype != MOE_IDS_INT32) return fail(MOE_EINVAL, "router mode writes int32 ids");
+    if (d->K > d->E) return fail(MOE_EINVAL, "top-k %d exceeds E %d", d->K, d->E);
+  }
+  if (d->token_block != 0 && d->token_block != 16 && d->token_block != 32)
+    return fail(MOE_EINVAL, "token_block must be 0, 16 or 32");
+  if (d->weight_format == MOE_WEIGHTS_W4G128) {
+    if (d->H % 128 || d->I % 128)
+      return fail(MOE_EINVAL, "W4G128 needs H %% 128 == 0 and I %% 128 == 0");
+    if (!shape_fast(d, choose_token_block(d)))
+      return fail(MOE_EINVAL, "W4G128 shape outside the MFMA path limits");
+  }
+  return MOE_OK;
+}
+
+moe_layout compute_layout(const moe_desc *d) {
+  moe_layout L;
+  memset(&L, 0, sizeof(L));
+  const size_t R = (size_t)d->T * d->K;
+  const int tb = choose_token_block(d);
+  const size_t cap = (R + tb - 1) / tb + (R < (size_t)d->E ? R : (size_t)d->E);
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align_up(o + bytes, 256);
+    return at;
+  };
+  L.status = take(2 * sizeof(uint32_t));
+  L.counts = take((size_t)d->E * 4);
+  L.offsets = take((size_t)d->E * 4);
+  L.ranks = take(R * 4);
+  L.map = take(R * 4);
+  L.row_route = take(R * 4);
+  L.tasks = take(cap * 16);
+  L.num_tasks = take(4);
+  L.act = take(R * (size_t)d->I * 2);
+  L.routed = take(R * (size_t)d->H * 2);
+  L.total = o;
+  L.task_capacity = (int32_t)cap;
+  L.token_block = tb;
+  const bool fuse = d->route_mode == MOE_ROUTE_LOGITS &&
+                    (long long)d->T * d->E <= kFuseRouterLogits;
+  L.fast_path = shape_fast(d, tb) ? 1 : 0;
+  if (d->T == 0)
+    L.launches = 0;
+  else
+    L.launches = 4 + (d->route_mode == MOE_ROUTE_LOGITS && !fuse ? 1 : 0);
+  return L;
+}
+
+}  // namespace
+
+struct moe_plan {
+  moe_desc d;
+  moe_layout L;
+  int device;
+  bool fuse_router;
+  bool fast;
+};
+
+extern "C" {
+
+int moe_abi_version(void) { return MOE_ABI_VERSION; }
+
+const char *moe_last_error(void) { return g_err; }
+
+int moe_workspace_layout(const moe_desc *d, moe_layout *out) {
+  int rc = validate(d);
+  if (rc) return rc;
+  if (!out) return fail(MOE_EINVAL, "null layout");
+  *out = compute_layout(d);
+  return MOE_OK;
+}
+
+int moe_plan_create(moe_plan **out, const moe_desc *d) {
+  if (!out) return fail(MOE_EINVAL, "null plan pointer");
+  *out = nullptr;
+  int rc = validate(d);
+  if (rc) return rc;
+  const moe_layout L = compute_layout(d);
+  if (d->T > 0) {
+    if (!d->x || !d->ids || !d->weights || !d->down || !d->out || !d->workspace)
+      return fail(MOE_EINVAL, "null tensor pointer");
+    if (d->route_mode == MOE_ROUTE_LOGITS && !d->logits)
+      return fail(MOE_EINVAL, "router mode needs logits");
+    if (d->weight_format == MOE_WEIGHTS_BF16 && !d->gate_up)
+      return fail(MOE_EINVAL, "null gate_up");
+    if (d->weight_format == MOE_WEIGHTS_W4G128 && (!d->w4_words || !d->w4_scales))
+      return fail(MOE_EINVAL, "null W4 words/scales");
+    if (((uintptr_t)d->workspace & 255u) != 0)
+      return fail(MOE_EINVAL, "workspace must be 256-byte aligned");
+    if (d->workspace_bytes < L.total)
+      return fail(MOE_ESPACE, "workspace has %zu bytes, needs %zu", d->workspace_bytes, L.total);
+  }
+  bool fast = L.fast_path != 0;
+  if (fast && !(aligned16(d->x) && aligned16(d->down) && aligned16(d->out) &&
+                (d->weight_format == MOE_WEIGHTS_W4G128 ? aligned16(d->w4_words)
+                                                        : aligned16(d->gate_up))))
+    fast = false;
+  if (!fast && d->weight_format == MOE_WEIGHTS_W4G128)
+    return fail(MOE_EINVAL, "W4G128 buffers must be 16-byte aligned");
+  moe_plan *p = new (std::nothrow) moe_plan;
+  if (!p) return fail(MOE_EINVAL, "out of host memory");
+  p->d = *d;
+  p->L = L;
+  p->L.fast_path = fast ? 1 : 0;
+  p->fast = fast;
+  p->fuse_router = d->route_mode == MOE_ROUTE_LOGITS &&
+                   (long long)d->T * d->E <= kFuseRouterLogits;
+  hipError_t e = hipGetDevice(&p->device);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "hipGetDevice");
+  }
+  *out = p;
+  return MOE_OK;
+}
+
+int moe_plan_layout(const moe_plan *p, moe_layout *out) {
+  if (!p || !out) return fail(MOE_EINVAL, "null argument");
+  *out = p->L;
+  return MOE_OK;
+}
+
+// Launch stages [first, last) of one forward.  Stage order:
+// [router] route_plan gate_up down combine.
+static int run_stages(moe_plan *p, int first, int last, void *stream) {
+  const moe_desc &d = p->d;
+  if (d.T == 0) return MOE_OK;
+  int prev = -1;
+  hipError_t e = hipGetDevice(&prev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (prev != p->device && (e = hipSetDevice(p->device)) != hipSuccess)
+    return hip_fail(e, "hipSetDevice");
+  hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)d.workspace;
+  const moe_layout &L = p->L;
+
+  moe::RouteArgs ra;
+  ra.logits = (const float *)d.logits;
+  ra.ids = d.ids;
+  ra.weights = (float *)d.weights;
+  ra.status = (uint32_t *)(ws + L.status);
+  ra.counts = (int32_t *)(ws + L.counts);
+  ra.offsets = (int32_t *)(ws + L.offsets);
+  ra.ranks = (int32_t *)(ws + L.ranks);
+  ra.map = (int32_t *)(ws + L.map);
+  ra.row_route = (int32_t *)(ws + L.row_route);
+  ra.tasks = (int4 *)(ws + L.tasks);
+  ra.num_tasks = (int32_t *)(ws + L.num_tasks);
+  ra.T = d.T;
+  ra.K = d.K;
+  ra.E = d.E;
+  ra.R = d.T * d.K;
+  ra.route_logits = d.route_mode == MOE_ROUTE_LOGITS;
+  ra.renormalize = d.renormalize;
+  ra.id64 = d.id_dtype == MOE_IDS_INT64;
+  ra.fuse_router = p->fuse_router;
+  ra.token_block = L.token_block;
+
+  moe::ExpertArgs xa;
+  xa.x = (const uint16_t *)d.x;
+  xa.gate_up = (const uint16_t *)d.gate_up;
+  xa.w4_words = (const uint32_t *)d.w4_words;
+  xa.w4_scales = (const uint16_t *)d.w4_scales;
+  xa.down = (const uint16_t *)d.down;
+  xa.weights = (const float *)d.weights;
+  xa.map = ra.map;
+  xa.row_route = ra.row_route;
+  xa.num_tasks = ra.num_tasks;
+  xa.tasks = ra.tasks;
+  xa.act = (uint16_t *)(ws + L.act);
+  xa.routed = (uint16_t *)(ws + L.routed);
+  xa.out = (uint16_t *)d.out;
+  xa.T = d.T;
+  xa.H = d.H;
+  xa.I = d.I;
+  xa.E = d.E;
+  xa.K = d.K;
+  xa.R = ra.R;
+
+  const bool w4 = d.weight_format == MOE_WEIGHTS_W4G128;
+  const bool router = ra.route_logits && !ra.fuse_router;
+  int rc = MOE_OK;
+  for (int st = first; st < last && rc == MOE_OK; ++st) {
+    const int kind = router ? st : st + 1;  // 0 router, 1 plan, 2 gate/up, 3 down, 4 combine
+    switch (kind) {
+      case 0: e = moe::launch_router(ra, s); break;
+      case 1: e = moe::launch_route_plan(ra, s); break;
+      case 2: e = moe::launch_gate_up(xa, L.task_capacity, L.token_block, w4, p->fast, s); break;
+      case 3: e = moe::launch_down(xa, L.task_capacity, L.token_block, p->fast, s); break;
+      default: e = moe::launch_combine(xa, s); break;
+    }
+    if (e != hipSuccess) {
+      static const char *names[] = {"router", "route plan", "gate/up", "down", "combine"};
+      rc = hip_fail(e, names[kind]);
+    }
+  }
+  if (prev != p->device) (void)hipSetDevice(prev);
+  return rc;
+}
+
+int moe_plan_run(moe_plan *p, void *stream) {
+  if (!p) return fail(MOE_EINVAL, "null plan");
+  return run_stages(p, 0, p->L.launches, stream);
+}
+
+int moe_plan_run_stage(moe_plan *p, int32_t stage, void *stream) {
+  if (!p) return fail(MOE_EINVAL, "null plan");
+  if (stage < 0 || stage >= p->L.launches)
+    return fail(MOE_EINVAL, "stage %d outside [0, %d)", stage, p->L.launches);
+  return run_stages(p, stage, stage + 1, stream);
+}
+
+int moe_plan_read_status(moe_plan *p, void *stream, uint32_t *flags) {
+  if (!p || !flags) return fail(MOE_EINVAL, "null argument");
+  *flags = 0;
+  if (p->d.T == 0) return MOE_OK;
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  const char *ws = (const char *)p->d.workspace;
+  e = hipMemcpy(flags, ws + p->L.status, sizeof(uint32_t), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "status readback");
+  return MOE_OK;
+}
+
+void moe_plan_destroy(moe_plan *p) { delete p; }
+
+int moe_w4_dequantize(const void *words_t, const void *scales_t, int32_t E, int32_t N, int32_t K,
+                      void *out_bf16, void *stream) {
+  if (E < 1 || N < 16 || N % 16 || K < 128 || K % 128)
+    return fail(MOE_EINVAL, "W4 dequantize needs N %% 16 == 0, K %% 128 == 0");
+  if (!words_t || !scales_t || !out_bf16 || !aligned16(words_t) || !aligned16(out_bf16))
+    return fail(MOE_EINVAL, "null or misaligned W4 buffer");
+  hipError_t e = moe::launch_w4_dequantize((const uint32_t *)words_t, (const uint16_t *)scales_t,
+                                           E, N, K, (uint16_t *)out_bf16, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "W4 dequantize launch");
+  return MOE_OK;
+}
+
+}  // extern "C"

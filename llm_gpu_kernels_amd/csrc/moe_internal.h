@@ -1,0 +1,58 @@
+// Internal launch interface between the C ABI layer and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+// Routing stage: router (optional), status, canonical ranks, scan, map, tasks.
+struct RouteArgs {
+  const float *logits;     // [T, E] (logits mode)
+  void *ids;               // [T, K] int32 / int64 (int32 output in logits mode)
+  float *weights;          // [T, K]
+  uint32_t *status;        // [2]: status bits, router flag word (self-clearing)
+  int32_t *counts, *offsets, *ranks, *map, *row_route;
+  int4 *tasks;             // {expert, first grouped row, rows, 0}
+  int32_t *num_tasks;
+  int T, K, E, R;
+  int route_logits, renormalize, id64, fuse_router;
+  int token_block;
+};
+
+// Expert stage: gate/up + SwiGLU, down projection, weighted combine.
+struct ExpertArgs {
+  const uint16_t *x;           // [T, H] bf16
+  const uint16_t *gate_up;     // [E, 2I, H] bf16
+  const uint32_t *w4_words;    // tiled int4 words
+  const uint16_t *w4_scales;   // tiled bf16 scales
+  const uint16_t *down;        // [E, H, I] bf16
+  const float *weights;        // [T, K]
+  const int32_t *map, *row_route, *num_tasks;
+  const int4 *tasks;
+  uint16_t *act;               // [R, I] bf16, grouped-row order
+  uint16_t *routed;            // [R, H] bf16, route order
+  uint16_t *out;               // [T, H] bf16
+  int T, H, I, E, K, R;
+};
+
+// Router kernel for large T (one wave per token); folds its flags into status[1].
+hipError_t launch_router(const RouteArgs &a, hipStream_t s);
+// Single-workgroup planner (fuses the router when a.fuse_router).
+hipError_t launch_route_plan(const RouteArgs &a, hipStream_t s);
+
+// token_block: 16 or 32 grouped rows per task.  fast: MFMA kernels (shape
+// constraints checked by the caller), otherwise the generic kernels.
+hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
+                          bool fast, hipStream_t s);
+hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, bool fast,
+                       hipStream_t s);
+hipError_t launch_combine(const ExpertArgs &a, hipStream_t s);
+hipError_t launch_w4_dequantize(const uint32_t *words_t, const uint16_t *scales_t, int E, int N,
+                                int K, uint16_t *out, hipStream_t s);
+
+size_t gate_up_lds_bytes(int H, int token_block);
+size_t down_lds_bytes(int I, int token_block);
+constexpr size_t kMaxLds = 160 * 1024;
+
+}  // namespace moe

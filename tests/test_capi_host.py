@@ -1,0 +1,162 @@
+"""C ABI checks that need no GPU: exports, validation, host-side W4 functions."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from llm_gpu_kernels_amd import _native as N
+from llm_gpu_kernels_amd import quantize_gate_up, tile_gate_up
+from oracle import moe_oracle as O
+
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+
+
+def _declared_functions():
+    names = set()
+    for header in INCLUDE.glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(\w+)\s*\([^;{]*\)\s*;", text, flags=re.M):
+            if not m.group(0).lstrip().startswith(("typedef", "#")):
+                names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_function():
+    lib = N.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    assert declared <= set(N.SIGNATURES), declared - set(N.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.moe_abi_version() == 1
+
+
+def test_struct_sizes_match_header():
+    # 10 int32 + 10 pointers + size_t; 11 size_t + 4 int32.
+    assert ctypes.sizeof(N.MoeDesc) == 40 + 8 * 10 + 8
+    assert ctypes.sizeof(N.MoeLayout) == 8 * 11 + 16
+
+
+def _desc(**kw):
+    d = N.MoeDesc()
+    d.T, d.H, d.I, d.E, d.K = kw.get("T", 17), kw.get("H", 2048), kw.get("I", 768), \
+        kw.get("E", 128), kw.get("K", 8)
+    d.weight_format = kw.get("fmt", N.WEIGHTS_BF16)
+    d.id_dtype = kw.get("ids", N.IDS_INT32)
+    d.route_mode = kw.get("route", N.ROUTE_FIXED)
+    d.token_block = kw.get("tb", 0)
+    return d
+
+
+def _layout(d):
+    lay = N.MoeLayout()
+    rc = N.lib().moe_workspace_layout(ctypes.byref(d), ctypes.byref(lay))
+    return rc, lay
+
+
+def test_layout_for_qwen_shape():
+    rc, lay = _layout(_desc())
+    assert rc == 0
+    r = 17 * 8
+    assert lay.token_block == 16 and lay.fast_path == 1 and lay.launches == 4
+    assert lay.task_capacity == (r + 15) // 16 + 128
+    assert lay.act % 256 == 0 and lay.routed % 256 == 0
+    assert lay.total >= lay.routed + r * 2048 * 2
+    rc, lay = _layout(_desc(T=1024))
+    assert lay.token_block == 32
+    rc, lay = _layout(_desc(T=0))
+    assert rc == 0 and lay.launches == 0
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=1024))
+    assert lay.launches == 5
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17))
+    assert lay.launches == 4
+    rc, lay = _layout(_desc(H=33, I=19, E=8, K=2))
+    assert rc == 0 and lay.fast_path == 0
+
+
+@pytest.mark.parametrize("kw", [dict(E=0), dict(E=257), dict(K=0), dict(K=33), dict(H=0),
+                                dict(I=-1), dict(T=-1), dict(fmt=7), dict(ids=9), dict(tb=8),
+                                dict(route=N.ROUTE_LOGITS, ids=N.IDS_INT64),
+                                dict(route=N.ROUTE_LOGITS, E=4, K=8),
+                                dict(fmt=N.WEIGHTS_W4G128, H=192),
+                                dict(T=2 ** 27, K=16)])
+def test_layout_rejects_invalid_descriptors(kw):
+    rc, _ = _layout(_desc(**kw))
+    assert rc == N.MOE_EINVAL
+    assert N.last_error()
+
+
+def test_plan_create_rejects_null_pointers():
+    d = _desc()
+    handle = ctypes.c_void_p()
+    rc = N.lib().moe_plan_create(ctypes.byref(handle), ctypes.byref(d))
+    assert rc == N.MOE_EINVAL and not handle.value
+    with pytest.raises(ValueError):
+        N.check(rc, "prepare")
+
+
+@pytest.mark.parametrize("shape", [(2, 16, 128), (3, 32, 384), (1, 48, 1024)])
+def test_quantize_matches_oracle_bit_exact(shape):
+    g = torch.Generator().manual_seed(sum(shape))
+    w = (torch.randn(shape, generator=g) * 0.02).to(torch.bfloat16)
+    w[0, 0, :128] = 0
+    w[0, 1, :8] = torch.tensor([7.0, -7.0, 3.5, 4.5, -3.5, 0.5, 1.5, -0.5]).to(torch.bfloat16) * 1e-2
+    p = quantize_gate_up(w.contiguous())
+    ow, os_ = O.quantize_w4(w)
+    assert torch.equal(p.words, ow)
+    assert torch.equal(p.scales.view(torch.int16), os_.view(torch.int16))
+
+
+def test_quantize_rejects_nonfinite():
+    w = torch.zeros((1, 16, 128), dtype=torch.bfloat16)
+    w[0, 3, 5] = float("nan")
+    with pytest.raises(ValueError):
+        quantize_gate_up(w)
+
+
+def test_tile_layout_index_map():
+    """words_t[e][rb][grp][lane][j] == v1 word 16*grp + 4*j + lane//16 of row 16*rb + lane%16."""
+    e, n, k = 2, 32, 256
+    words = torch.arange(e * n * k // 8, dtype=torch.int32).reshape(e, n, k // 8)
+    scales = torch.arange(e * n * k // 128, dtype=torch.int16).view(torch.bfloat16).reshape(e, n, k // 128)
+    t = tile_gate_up(O_packed(words, scales))
+    for ei, rb, grp, lane, j in [(0, 0, 0, 0, 0), (1, 1, 1, 63, 3), (0, 1, 0, 17, 2), (1, 0, 1, 40, 1)]:
+        r, g = lane % 16, lane // 16
+        assert t.words[ei, rb, grp, lane, j] == words[ei, rb * 16 + r, 16 * grp + 4 * j + g]
+        assert t.scales[ei, rb, grp, r].view(torch.int16) == scales[ei, rb * 16 + r, grp].view(torch.int16)
+    assert sorted(t.words.reshape(-1).tolist()) == list(range(e * n * k // 8))
+
+
+def O_packed(words, scales):
+    from llm_gpu_kernels_amd.weight_quant import PackedGateUp
+    return PackedGateUp(words, scales, {})
+
+
+def test_tile_emulated_decode_matches_oracle_dequant():
+    """Host emulation of the kernel's (16+n)*s - 24*s decode on the tiled layout."""
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn((2, 32, 256), generator=g) * 0.03).to(torch.bfloat16)
+    p = quantize_gate_up(w)
+    t = tile_gate_up(p)
+    ref = O.dequantize_w4(p.words, p.scales)
+    e, n, k = 2, 32, 256
+    out = torch.empty((e, n, k), dtype=torch.bfloat16)
+    wt = t.words.to(torch.int64) & 0xFFFFFFFF
+    st = t.scales.float()
+    for ei in range(e):
+        for rb in range(n // 16):
+            for grp in range(k // 128):
+                for lane in range(64):
+                    r, gg = lane % 16, lane // 16
+                    s = st[ei, rb, grp, r]
+                    for j in range(4):
+                        wd = int(wt[ei, rb, grp, lane, j])
+                        for i in range(8):
+                            nib = (wd >> (4 * i)) & 15
+                            f = torch.tensor(16.0 + nib, dtype=torch.float32)
+                            val = (f * s).double() - 24 * s.double()  # exact, as fma
+                            out[ei, rb * 16 + r, grp * 128 + 32 * j + 8 * gg + i] = \
+                                torch.tensor(float(val), dtype=torch.float32).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))

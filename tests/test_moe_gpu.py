@@ -1,0 +1,207 @@
+"""Parity of the HIP MoE forward against the CPU oracle (MI355X only).
+
+Bit-exact: router IDs, counts, offsets, canonical ranks, map, its inverse,
+the task list and W4 dequantised values.  Tolerance (rel-RMS <= 5e-3,
+normalised max <= 1e-2) for layer outputs against the FP32 oracle; the
+reference's functional specs (N(0,1) weights) use the reference's own
+0.008/0.008 limits against the FP32 oracle plus a tight check against the
+rounding-staged oracle.
+"""
+import json
+from pathlib import Path
+
+import pytest
+import torch
+
+from llm_gpu_kernels_amd import (GemmConfig, dequantize_tiled, prepare_moe, prepare_routed_moe,
+                                 prepare_w4_moe, quantize_gate_up, tile_gate_up)
+from llm_gpu_kernels_amd.workloads import make_layer
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "m4_reference_records.json").read_text())
+FUNCTIONAL = [c for c in GOLDEN["cases"] if c["family"] == "functional_cases"]
+SMALL_PERF = [c for c in GOLDEN["cases"] if c["family"] == "performance_cases" and c["E"] == 16]
+DT = {"torch.int32": torch.int32, "torch.int64": torch.int64}
+REF_LIMITS = {"relative_rms": 0.008, "normalized_max": 0.008}
+STAGED_LIMITS = {"relative_rms": 2e-3, "normalized_max": 8e-3}
+
+
+def _to(dev, *ts):
+    return [t.to(dev) for t in ts]
+
+
+def _check_dispatch(plan, ids_cpu, experts):
+    d = O.canonical_dispatch(ids_cpu, experts)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.counts.cpu(), d["counts"])
+    assert torch.equal(plan.offsets.cpu(), d["offsets"])
+    assert torch.equal(plan.ranks.cpu(), d["ranks"])
+    assert torch.equal(plan.mapping.cpu(), d["map"])
+    assert torch.equal(plan.row_route.cpu(), d["row_route"])
+    # Task list: expert-major blocks of token_block rows covering every row once.
+    tb = plan.layout.token_block
+    n = int(plan.num_tasks.item())
+    tasks = plan.tasks[:n].cpu().tolist()
+    expect = []
+    for e in range(experts):
+        c, off = int(d["counts"][e]), int(d["offsets"][e])
+        expect += [[e, off + r0, min(tb, c - r0), 0] for r0 in range(0, c, tb)]
+    assert tasks == expect
+
+
+@pytest.mark.parametrize("case", FUNCTIONAL + SMALL_PERF, ids=lambda c: c["name"])
+def test_reference_functional_specs(case, gpu_device):
+    x, gu, dn, ids, rw = O.make_inputs(tokens=case["T"], experts=case["E"], topk=case["topk"],
+                                       hidden=case["H"], intermediate=case["I"],
+                                       id_dtype=DT[case["id_dtype"]], pattern=case["route_pattern"],
+                                       seed=case["seed"], signed_weights=case.get("signed_weights", False))
+    assert O.tensor_hash(ids) == case["routing_sha256"]
+    dev = _to(gpu_device, x, gu, dn, ids, rw)
+    plan = prepare_moe(*dev)
+    out = plan.run()
+    torch.cuda.synchronize()
+    assert out.shape == (case["T"], case["H"]) and out.dtype == torch.bfloat16
+    if case["T"] == 0:
+        assert plan.launches == ()
+        return
+    plan.check_inputs()
+    _check_dispatch(plan, ids, case["E"])
+    m32 = O.error(out, O.moe_reference(x, gu, dn, ids, rw), REF_LIMITS)
+    ms = O.error(out, O.staged_bf16_oracle(x, gu, dn, ids, rw), STAGED_LIMITS)
+    assert m32["passed"], m32
+    assert ms["passed"], ms
+
+
+@pytest.mark.parametrize("block", [16, 32])
+def test_token_block_invariance(block, gpu_device):
+    """Each grouped row's arithmetic is independent of the task size: bitwise equal."""
+    lay = make_layer("qwen", 193, seed=3, device=gpu_device)
+    ids, w = O.route_topk(lay["logits"].cpu(), 8)
+    args = (lay["x"], lay["gate_up"], lay["down"], ids.to(gpu_device), w.to(gpu_device))
+    a = prepare_moe(*args, config=GemmConfig(block_m=block)).run().clone()
+    b = prepare_moe(*args, config=GemmConfig(block_m=48 - block)).run().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+CONFIGS = [("tiny", 17, "uniform"), ("qwen", 17, "uniform"), ("qwen", 193, "uniform"),
+           ("qwen", 1024, "zipf"), ("qwen", 1024, "uniform")]
+
+
+def _routed_parity(shape, tokens, routing, gpu_device, w4=False):
+    lay = make_layer(shape, tokens, routing=routing, seed=0, device=gpu_device)
+    k = lay["K"]
+    gate_up = lay["gate_up"]
+    if w4:
+        packed = quantize_gate_up(gate_up.cpu())
+        tiled = tile_gate_up(packed).to(gpu_device)
+        deq = dequantize_tiled(tiled)
+        torch.cuda.synchronize()
+        ref_deq = O.dequantize_w4(packed.words, packed.scales)
+        assert torch.equal(deq.cpu().view(torch.int16), ref_deq.view(torch.int16))
+        weights_for_oracle = ref_deq
+        gate_up = tiled
+    else:
+        weights_for_oracle = gate_up.cpu()
+    plan = prepare_routed_moe(lay["x"], lay["logits"], gate_up, lay["down"], k)
+    out = plan.forward(lay["x"], lay["logits"])
+    torch.cuda.synchronize()
+    plan.check_inputs()
+    logits = lay["logits"].cpu()
+    ids, w = O.route_topk(logits, k)
+    assert torch.equal(plan.ids.cpu(), ids), "router IDs differ"
+    assert torch.allclose(plan.routing_weights.cpu(), w, rtol=2e-6, atol=1e-7)
+    _check_dispatch(plan, ids, lay["E"])
+    x, dn = lay["x"].cpu(), lay["down"].cpu()
+    m = O.error(out, O.moe_reference(x, weights_for_oracle, dn, ids, w))
+    assert m["passed"], m
+    return plan
+
+
+@pytest.mark.parametrize("shape,tokens,routing", CONFIGS, ids=lambda v: str(v))
+def test_routed_bf16_layer(shape, tokens, routing, gpu_device):
+    _routed_parity(shape, tokens, routing, gpu_device)
+
+
+@pytest.mark.parametrize("tokens", [17, 193, 1024])
+def test_routed_w4_layer(tokens, gpu_device):
+    _routed_parity("qwen", tokens, "uniform", gpu_device, w4=True)
+
+
+def test_status_bits(gpu_device):
+    x, gu, dn, ids, rw = O.make_inputs(tokens=3, experts=4, topk=2, hidden=128, intermediate=128,
+                                       id_dtype=torch.int32, pattern="random", seed=101)
+    x, gu, dn, ids, rw = _to(gpu_device, x, gu, dn, ids, rw)
+    plan = prepare_moe(x, gu, dn, ids, rw)
+    plan.check_inputs()
+    ids[0, 0] = 4
+    plan.run()
+    assert plan.read_status() == 1
+    with pytest.raises(ValueError):
+        plan.check_inputs()
+    rw[1, 1] = float("nan")
+    plan.run()
+    assert plan.read_status() == 3
+    ids[0, 0] = 1
+    plan.run()
+    assert plan.read_status() == 2
+    rw[1, 1] = 0.5
+    plan.run()
+    assert plan.read_status() == 0
+    # Router mode: a NaN logit sets bit 2 (and the weights it poisons bit 1).
+    lay = make_layer("tiny", 5, device=gpu_device)
+    p2 = prepare_routed_moe(lay["x"], lay["logits"], lay["gate_up"], lay["down"], 2)
+    p2.check_inputs()
+    lay["logits"][2, 3] = float("nan")
+    p2.forward()
+    assert p2.read_status() & 4
+
+
+def test_empty_tokens(gpu_device):
+    x, gu, dn, ids, rw = O.make_inputs(tokens=0, experts=8, topk=2, hidden=128, intermediate=128,
+                                       id_dtype=torch.int32, pattern="random", seed=1)
+    plan = prepare_moe(*_to(gpu_device, x, gu, dn, ids, rw))
+    assert plan.launches == () and plan.run().shape == (0, 128)
+
+
+def test_graph_capture_with_in_place_updates(gpu_device):
+    """Graph replays follow in-place value updates (docs/MOE_USAGE.md:126-180)."""
+    lay = make_layer("qwen", 17, seed=5, device=gpu_device)
+    plan = prepare_routed_moe(lay["x"], lay["logits"], lay["gate_up"], lay["down"], 8)
+    for _ in range(3):
+        plan.run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=gpu_device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(4):
+            gout = plan.run()
+    for step in range(3):
+        nxt = make_layer("qwen", 17, seed=100 + step, device=gpu_device, weights=False)
+        lay["x"].copy_(nxt["x"])
+        lay["logits"].copy_(nxt["logits"])
+        graph.replay()
+        torch.cuda.synchronize()
+        replay = gout.clone()
+        eager = plan.run().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(replay.view(torch.int16), eager.view(torch.int16))
+        ids, _ = O.route_topk(nxt["logits"].cpu(), 8)
+        assert torch.equal(plan.ids.cpu(), ids)
+    plan.check_inputs()
+
+
+def test_non_default_stream(gpu_device):
+    lay = make_layer("tiny", 33, seed=9, device=gpu_device)
+    plan = prepare_routed_moe(lay["x"], lay["logits"], lay["gate_up"], lay["down"], 2)
+    base = plan.run().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=gpu_device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = plan.run().clone()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(base.view(torch.int16), out.view(torch.int16))
