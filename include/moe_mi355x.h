@@ -75,7 +75,7 @@ typedef struct moe_desc {
   size_t workspace_bytes;
 } moe_desc;
 
-/* Byte offsets of the inspectable workspace arrays (all int32). */
+/* Byte offsets of the inspectable workspace arrays (int32 unless noted). */
 typedef struct moe_layout {
   size_t status;      /* [1]  uint32 status bits                                 */
   size_t counts;      /* [E]  routes per expert                                  */
@@ -83,8 +83,10 @@ typedef struct moe_layout {
   size_t ranks;       /* [R]  expert-local rank of route q = t*K + s (-1: bad id) */
   size_t map;         /* [R]  grouped row of route q (-1: bad id)                */
   size_t row_route;   /* [R]  route of grouped row p (inverse of map)            */
+  size_t row_token;   /* [R]  token of grouped row p (row_route[p] / K)          */
   size_t tasks;       /* [task_capacity][4] {expert, first row, rows, 0}         */
   size_t num_tasks;   /* [1]                                                     */
+  size_t counters;    /* [2]  work counters of the streaming GEMMs               */
   size_t act;         /* [R, I] bf16 SwiGLU activations in grouped-row order     */
   size_t routed;      /* [R, H] bf16 down projections in route order             */
   size_t total;       /* workspace bytes                                          */

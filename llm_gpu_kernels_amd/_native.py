@@ -28,8 +28,8 @@ class MoeDesc(ctypes.Structure):
 
 class MoeLayout(ctypes.Structure):
     _fields_ = [(name, c_size_t) for name in
-                ("status", "counts", "offsets", "ranks", "map", "row_route", "tasks",
-                 "num_tasks", "act", "routed", "total")] + \
+                ("status", "counts", "offsets", "ranks", "map", "row_route", "row_token", "tasks",
+                 "num_tasks", "counters", "act", "routed", "total")] + \
                [("task_capacity", c_int32), ("token_block", c_int32), ("launches", c_int32),
                 ("fast_path", c_int32)]
 

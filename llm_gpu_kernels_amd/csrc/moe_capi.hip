@@ -33,8 +33,9 @@ int hip_fail(hipError_t e, const char *what) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Router fused into the planner's single workgroup up to this many logits.
-constexpr long long kFuseRouterLogits = 64 * 1024;
+// Router fused into the planner's single workgroup (16 waves) up to this many
+// tokens; beyond it a separate one-wave-per-token launch is faster.
+constexpr int kFuseRouterTokens = 64;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -45,12 +46,8 @@ int choose_token_block(const moe_desc *d) {
   return r <= 16LL * d->E ? 16 : 32;
 }
 
-bool shape_fast(const moe_desc *d, int tb) {
-  if (d->H % 128 || d->I % 128) return false;
-  if (moe::gate_up_lds_bytes(d->H, tb) > moe::kMaxLds) return false;
-  if (moe::down_lds_bytes(d->I, tb) > moe::kMaxLds) return false;
-  if (d->H > 4096 || d->I > 4096) return false;
-  return true;
+bool shape_fast(const moe_desc *d, int) {
+  return moe::stream_shape_ok(d->H, d->I, d->weight_format == MOE_WEIGHTS_W4G128);
 }
 
 int validate(const moe_desc *d) {
@@ -76,10 +73,8 @@ int validate(const moe_desc *d) {
   if (d->token_block != 0 && d->token_block != 16 && d->token_block != 32)
     return fail(MOE_EINVAL, "token_block must be 0, 16 or 32");
   if (d->weight_format == MOE_WEIGHTS_W4G128) {
-    if (d->H % 128 || d->I % 128)
-      return fail(MOE_EINVAL, "W4G128 needs H %% 128 == 0 and I %% 128 == 0");
     if (!shape_fast(d, choose_token_block(d)))
-      return fail(MOE_EINVAL, "W4G128 shape outside the MFMA path limits");
+      return fail(MOE_EINVAL, "W4G128 needs H %% 1024 == 0, I %% 256 == 0, H, I <= 4096");
   }
   return MOE_OK;
 }
@@ -101,16 +96,17 @@ moe_layout compute_layout(const moe_desc *d) {
   L.offsets = take((size_t)d->E * 4);
   L.ranks = take(R * 4);
   L.map = take(R * 4);
-  L.row_route = take(R * 4);
+  L.row_route = take(R * 4 + 32 * 4);  // slack: 32-row scalar reads past R
+  L.row_token = take(R * 4 + 32 * 4);
   L.tasks = take(cap * 16);
   L.num_tasks = take(4);
+  L.counters = take(2 * 4);
   L.act = take(R * (size_t)d->I * 2);
   L.routed = take(R * (size_t)d->H * 2);
   L.total = o;
   L.task_capacity = (int32_t)cap;
   L.token_block = tb;
-  const bool fuse = d->route_mode == MOE_ROUTE_LOGITS &&
-                    (long long)d->T * d->E <= kFuseRouterLogits;
+  const bool fuse = d->route_mode == MOE_ROUTE_LOGITS && d->T <= kFuseRouterTokens;
   L.fast_path = shape_fast(d, tb) ? 1 : 0;
   if (d->T == 0)
     L.launches = 0;
@@ -125,6 +121,7 @@ struct moe_plan {
   moe_desc d;
   moe_layout L;
   int device;
+  int num_cus;
   bool fuse_router;
   bool fast;
 };
@@ -176,12 +173,13 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
   p->L = L;
   p->L.fast_path = fast ? 1 : 0;
   p->fast = fast;
-  p->fuse_router = d->route_mode == MOE_ROUTE_LOGITS &&
-                   (long long)d->T * d->E <= kFuseRouterLogits;
+  p->fuse_router = d->route_mode == MOE_ROUTE_LOGITS && d->T <= kFuseRouterTokens;
   hipError_t e = hipGetDevice(&p->device);
+  if (e == hipSuccess)
+    e = hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
   if (e != hipSuccess) {
     delete p;
-    return hip_fail(e, "hipGetDevice");
+    return hip_fail(e, "device query");
   }
   *out = p;
   return MOE_OK;
@@ -217,8 +215,10 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   ra.ranks = (int32_t *)(ws + L.ranks);
   ra.map = (int32_t *)(ws + L.map);
   ra.row_route = (int32_t *)(ws + L.row_route);
+  ra.row_token = (int32_t *)(ws + L.row_token);
   ra.tasks = (int4 *)(ws + L.tasks);
   ra.num_tasks = (int32_t *)(ws + L.num_tasks);
+  ra.counters = (int32_t *)(ws + L.counters);
   ra.T = d.T;
   ra.K = d.K;
   ra.E = d.E;
@@ -238,8 +238,10 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   xa.weights = (const float *)d.weights;
   xa.map = ra.map;
   xa.row_route = ra.row_route;
+  xa.row_token = ra.row_token;
   xa.num_tasks = ra.num_tasks;
   xa.tasks = ra.tasks;
+  xa.counters = ra.counters;
   xa.act = (uint16_t *)(ws + L.act);
   xa.routed = (uint16_t *)(ws + L.routed);
   xa.out = (uint16_t *)d.out;
@@ -258,8 +260,12 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
     switch (kind) {
       case 0: e = moe::launch_router(ra, s); break;
       case 1: e = moe::launch_route_plan(ra, s); break;
-      case 2: e = moe::launch_gate_up(xa, L.task_capacity, L.token_block, w4, p->fast, s); break;
-      case 3: e = moe::launch_down(xa, L.task_capacity, L.token_block, p->fast, s); break;
+      case 2:
+        e = moe::launch_gate_up(xa, L.task_capacity, L.token_block, w4, p->fast, p->num_cus, s);
+        break;
+      case 3:
+        e = moe::launch_down(xa, L.task_capacity, L.token_block, p->fast, p->num_cus, s);
+        break;
       default: e = moe::launch_combine(xa, s); break;
     }
     if (e != hipSuccess) {

@@ -13,8 +13,10 @@ struct RouteArgs {
   float *weights;          // [T, K]
   uint32_t *status;        // [2]: status bits, router flag word (self-clearing)
   int32_t *counts, *offsets, *ranks, *map, *row_route;
+  int32_t *row_token;      // [R] token of grouped row p (row_route[p] / K)
   int4 *tasks;             // {expert, first grouped row, rows, 0}
   int32_t *num_tasks;
+  int32_t *counters;       // [2] work counters of the streaming GEMMs (zeroed here)
   int T, K, E, R;
   int route_logits, renormalize, id64, fuse_router;
   int token_block;
@@ -28,8 +30,9 @@ struct ExpertArgs {
   const uint16_t *w4_scales;   // tiled bf16 scales
   const uint16_t *down;        // [E, H, I] bf16
   const float *weights;        // [T, K]
-  const int32_t *map, *row_route, *num_tasks;
+  const int32_t *map, *row_route, *row_token, *num_tasks;
   const int4 *tasks;
+  int32_t *counters;           // [2] work counters (gate/up, down)
   uint16_t *act;               // [R, I] bf16, grouped-row order
   uint16_t *routed;            // [R, H] bf16, route order
   uint16_t *out;               // [T, H] bf16
@@ -44,15 +47,18 @@ hipError_t launch_route_plan(const RouteArgs &a, hipStream_t s);
 // token_block: 16 or 32 grouped rows per task.  fast: MFMA kernels (shape
 // constraints checked by the caller), otherwise the generic kernels.
 hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
-                          bool fast, hipStream_t s);
+                          bool fast, int num_cus, hipStream_t s);
 hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, bool fast,
-                       hipStream_t s);
+                       int num_cus, hipStream_t s);
+hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
+                                 int num_cus, hipStream_t s);
+hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,
+                              int num_cus, hipStream_t s);
+bool stream_shape_ok(int H, int I, bool w4);
 hipError_t launch_combine(const ExpertArgs &a, hipStream_t s);
 hipError_t launch_w4_dequantize(const uint32_t *words_t, const uint16_t *scales_t, int E, int N,
                                 int K, uint16_t *out, hipStream_t s);
 
-size_t gate_up_lds_bytes(int H, int token_block);
-size_t down_lds_bytes(int I, int token_block);
 constexpr size_t kMaxLds = 160 * 1024;
 
 }  // namespace moe

@@ -23,73 +23,103 @@ constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / kWave;
 constexpr int kMaxExperts = 256;
 
+// Wave-wide reductions from DPP row permutes (quad xor 1, quad xor 2, half-row
+// mirror, row mirror) and four v_readlane: every lane gets the result.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+}
+#define MOE_DPP_REDUCE(T, OP, TOBITS, FROMBITS)                                   \
+  v = OP(v, FROMBITS(dpp_u<0xb1>(TOBITS(v))));                                     \
+  v = OP(v, FROMBITS(dpp_u<0x4e>(TOBITS(v))));                                     \
+  v = OP(v, FROMBITS(dpp_u<0x141>(TOBITS(v))));                                    \
+  v = OP(v, FROMBITS(dpp_u<0x140>(TOBITS(v))));                                    \
+  {                                                                               \
+    const T a0 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 0));  \
+    const T a1 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 16)); \
+    const T a2 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 32)); \
+    const T a3 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 48)); \
+    v = OP(OP(a0, a1), OP(a2, a3));                                               \
+  }
+#define MOE_ID(x) (x)
+__device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t umin_(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ float fadd_(float a, float b) { return a + b; }
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+  MOE_DPP_REDUCE(uint32_t, umax_, MOE_ID, MOE_ID)
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_umin(uint32_t v) {
+  MOE_DPP_REDUCE(uint32_t, umin_, MOE_ID, MOE_ID)
+  return v;
+}
+__device__ __forceinline__ float wave_fsum(float v) {
+  MOE_DPP_REDUCE(float, fadd_, __float_as_uint, __uint_as_float)
+  return v;
+}
+#undef MOE_DPP_REDUCE
+#undef MOE_ID
+
+// Order-preserving map of a float to uint32 (NaN -> 0, below -inf).
+__device__ __forceinline__ uint32_t float_key(float f) {
+  if (isnan(f)) return 0u;
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // One wave routes token t.  Expert e lives in lane e % 64, slot e / 64.
-// Selection is by logit (softmax is monotone), largest first, ties to the
-// lower expert index; NaN logits sort below every number.
+// Selection is by logit (softmax is monotone): K rounds of a wave max over
+// the remaining keys, then the lowest expert index holding that key, so the
+// top-k come out in slot order with ties to the lower index.  NaN logits
+// rank below every number and set the logit flag.
 __device__ void route_token(const float *__restrict__ logits, int t, int E, int K,
                             int renormalize, int32_t *__restrict__ ids_out,
                             float *__restrict__ w_out, uint32_t &flags) {
   const int lane = threadIdx.x & (kWave - 1);
-  float raw[4], key[4];
+  float raw[4];
+  uint32_t key[4];
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane + kWave * j;
-    if (e < E) {
-      const float v = logits[(size_t)t * E + e];
-      bad |= !isfinite(v);
-      raw[j] = v;
-      key[j] = isnan(v) ? -INFINITY : v;
-    } else {
-      raw[j] = -INFINITY;
-      key[j] = -INFINITY;
-    }
+    raw[j] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
+    bad |= (e < E) && !isfinite(raw[j]);
+    key[j] = e < E ? float_key(raw[j]) : 0u;
   }
-  float m = fmaxf(fmaxf(key[0], key[1]), fmaxf(key[2], key[3]));
-  m = wave_max(m);
+  if (__any(bad)) flags |= 4u;
+  uint32_t top = umax_(umax_(key[0], key[1]), umax_(key[2], key[3]));
+  const float m = key_float(wave_umax(top));
   float z = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     if (lane + kWave * j < E) z += expf(raw[j] - m);
-  z = wave_sum(z);
-  if (__any(bad)) flags |= 4u;
+  z = wave_fsum(z);
 
   uint32_t taken = 0;
-  float my_p = 0.f;
+  float my_p = 0.f, psum = 0.f;
   int my_id = 0;
-  float psum = 0.f;
   for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    uint32_t best = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (!((taken >> j) & 1)) best = umax_(best, key[j]);
+    const uint32_t M = wave_umax(best);
+    uint32_t cand = 0xffffu;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = lane + kWave * j;
-      if (e < E && !(taken & (1u << j)) && (key[j] > bv || (key[j] == bv && e < bi))) {
-        bv = key[j];
-        bi = e;
-      }
+      if (e < E && !((taken >> j) & 1) && key[j] == M) cand = umin_(cand, (uint32_t)e);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, kWave);
-      const int oi = __shfl_xor(bi, o, kWave);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & (kWave - 1)) == lane) taken |= 1u << (bi / kWave);
-    const float rv = __shfl(raw[0], bi & (kWave - 1), kWave);
-    const float rv1 = __shfl(raw[1], bi & (kWave - 1), kWave);
-    const float rv2 = __shfl(raw[2], bi & (kWave - 1), kWave);
-    const float rv3 = __shfl(raw[3], bi & (kWave - 1), kWave);
-    const int slot = bi / kWave;
-    const float xv = slot == 0 ? rv : slot == 1 ? rv1 : slot == 2 ? rv2 : rv3;
-    const float p = expf(xv - m) / z;
+    const int idx = (int)wave_umin(cand);
+    if ((idx & (kWave - 1)) == lane) taken |= 1u << (idx / kWave);
+    const float p = expf(key_float(M) - m) / z;
     psum += p;
     if (lane == k) {
       my_p = p;
-      my_id = bi;
+      my_id = idx;
     }
   }
   if (lane < K) {
@@ -227,11 +257,15 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
       const int p = s_off[idv] + a.ranks[q];
       a.map[q] = p;
       a.row_route[p] = q;
+      a.row_token[p] = q / a.K;
     } else {
       a.map[q] = -1;
     }
   }
-  for (int p = valid_rows + tid; p < a.R; p += kPlanThreads) a.row_route[p] = -1;
+  for (int p = valid_rows + tid; p < a.R; p += kPlanThreads) {
+    a.row_route[p] = -1;
+    a.row_token[p] = 0;
+  }
 
   // Pass 4: task list, expert-major.
   for (int e = tid; e < E; e += kPlanThreads) {
@@ -246,6 +280,8 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   if (tid == 0) {
     *a.num_tasks = s_toff[E];
     a.status[0] = s_status;
+    a.counters[0] = 0;
+    a.counters[1] = 0;
   }
 }
 

@@ -1,0 +1,329 @@
+// Weight-streaming grouped GEMMs of the MoE forward on gfx950 (CDNA4).
+//
+// gate/up + SwiGLU (reference: _dynamic_grouped_gate_up_swiglu,
+// moe_fused.py:18-73; cuda_gate_up_bf16, cuda_gate_up.cu:53-131; W4:
+// cuda_gate_up_w4_sync, cuda_w4_gate_up.cu:46-100) and the down projection
+// (_dynamic_grouped, moe.py:69-95) for the regime of every BASELINE
+// configuration: few grouped rows per expert, so the expert weights are the
+// only large operand and the kernel is bound by HBM bandwidth.
+//
+// Work unit = (task, column block): a task is an expert and up to 16*MT of
+// its grouped rows; a column block is 16 intermediate columns (gate/up
+// kernel: 16 gate rows + 16 up rows of weights) or 32 hidden columns (down).
+//
+//  * Split-K across the 8 waves of a workgroup: wave w owns k-steps
+//    [w*SPW, (w+1)*SPW).  It loads its K-slice of the unit's token rows (MFMA
+//    B operand) straight from global memory into registers -- x rows are
+//    gathered through the route list, no permuted copy of x exists -- and
+//    streams the weights (MFMA A operand, one 128-bit load per lane per
+//    16x16x32 MFMA) from HBM.  The eight partial tiles are summed through LDS
+//    in fixed wave order (deterministic) and the epilogue applies the
+//    reference's rounding stages.
+//  * Persistent workgroups, one per CU slot, take units round-robin
+//    (balanced to one unit).  The next unit's weights are in flight while the
+//    current unit multiplies.  The loop body is straight-line: k-slices are
+//    compile-time, invalid rows load a clamped address and are zeroed, and
+//    all unit metadata comes through scalar loads, so the only vector-memory
+//    wait before the MFMAs is for the current unit's operands.
+//  * W4G128: the 16-byte load of a lane holds 32 int4 of one row (a whole
+//    128-K group, 4 MFMA k-steps) and is decoded in registers by
+//    w4_decode8, bit-exact with the reference dequantisation.
+#include "common.h"
+#include "moe_internal.h"
+
+#define MOE_CONST __attribute__((address_space(4)))
+
+namespace moe {
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+
+template <typename T>
+__device__ __forceinline__ const MOE_CONST T *as_const(const T *p) {
+  return (const MOE_CONST T *)p;
+}
+
+// Workgroup barrier ordering LDS only.  __syncthreads() also orders global
+// memory, which makes every wave wait for its in-flight weight prefetch.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// KIND 0: gate/up + SwiGLU.  A = gate rows cb*16.. and up rows I+cb*16..,
+//         K = H, B = x rows of the task's tokens.
+// KIND 1: down.  A = rows cb*32 + 16*rb (rb < 2), K = I, B = act rows.
+template <int KIND, int MT, int SPW, bool W4>
+__global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
+  constexpr int NRB = 2;
+  constexpr int ROWS = 16 * MT;
+  extern __shared__ f32x4 s_red[];  // [2][kWaves][NRB][MT][64]
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & (kWave - 1);
+  const int r = lane & 15, g = lane >> 4;
+  const int H = a.H, I = a.I;
+  const int s0 = wave * SPW;
+  const int ncb = KIND == 0 ? I / 16 : H / 32;
+  const int total = *as_const(a.num_tasks) * ncb;
+  // Units are dealt round-robin (unit b, b+G, ...): at any moment the G
+  // workgroups stream adjacent units, i.e. the chip sweeps the weights in
+  // address order, instead of each workgroup walking its own block in
+  // lockstep with the others (which concentrates on few HBM channels).
+  const int G = gridDim.x;
+  const int u_begin = blockIdx.x;
+  if (u_begin >= total) return;
+
+  const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
+  const MOE_CONST int32_t *row_idx = as_const(KIND == 0 ? a.row_token : a.row_route);
+
+  // Unit metadata: scalars, plus one VGPR whose lane k < ROWS holds the
+  // token (gate/up) or route (down) of the task's row k, built with
+  // lane selects from scalar loads and read back with a lane shuffle.
+  struct Meta {
+    int unit, cb, expert, row0, rows;
+    int idxv;
+  };
+  auto meta_of = [&](int u) {
+    Meta m;
+    m.unit = u;
+    const int t = u / ncb;
+    m.cb = u - t * ncb;
+    m.expert = tasks[4 * t];
+    m.row0 = tasks[4 * t + 1];
+    m.rows = tasks[4 * t + 2];
+    int v = 0;
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {  // in-bounds: the index arrays carry 32 ints of slack
+      const int sv = row_idx[m.row0 + k];
+      v = lane == k ? sv : v;
+    }
+    m.idxv = v;
+    return m;
+  };
+
+  // B operand: [MT][SPW] fragments of this wave's K-slice.
+  u32x4 bfr[MT][SPW];
+  auto load_b = [&](const Meta &m) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int j = mt * 16 + r;
+      const bool ok = j < m.rows;
+      size_t row;
+      if (KIND == 0)
+        row = (size_t)(ok ? __shfl(m.idxv, j, kWave) : 0) * H;
+      else
+        row = (size_t)(ok ? m.row0 + j : 0) * I;
+      const uint16_t *src = (KIND == 0 ? a.x : a.act) + row + s0 * 32 + g * 8;
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const u32x4 v = *(const u32x4 *)(src + i * 32);
+        bfr[mt][i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  // A operand: bf16 -> [NRB][SPW] fragments; W4 -> [NRB][SPW/4] words + scales.
+  constexpr int AW = W4 ? SPW / 4 : SPW;
+  u32x4 abuf[NRB][AW], nbuf[NRB][AW];
+  uint32_t ascale[NRB][AW], nscale[NRB][AW];
+  auto load_a = [&](const Meta &m, u32x4 (&buf)[NRB][AW], uint32_t (&sc)[NRB][AW]) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      if constexpr (W4) {
+        const int G = H >> 7;
+        const size_t rbi = (size_t)m.expert * (2 * I / 16) + m.cb + (rb ? I / 16 : 0);
+#pragma unroll
+        for (int i = 0; i < AW; ++i) {
+          const size_t unit = rbi * G + (s0 >> 2) + i;
+          buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + lane];
+          sc[rb][i] = a.w4_scales[unit * 16 + r];
+        }
+      } else {
+        const uint16_t *row;
+        if (KIND == 0)
+          row = a.gate_up + ((size_t)m.expert * 2 * I + (rb ? I : 0) + m.cb * 16 + r) * H;
+        else
+          row = a.down + ((size_t)m.expert * H + m.cb * 32 + rb * 16 + r) * I;
+        row += s0 * 32 + g * 8;
+#pragma unroll
+        for (int i = 0; i < AW; ++i) buf[rb][i] = *(const u32x4 *)(row + i * 32);
+      }
+    }
+  };
+
+  Meta cur = meta_of(u_begin);
+  load_a(cur, abuf, ascale);
+  load_b(cur);
+  int buf = 0;
+
+  for (int u = u_begin; u < total; u += G) {
+    // Next unit (the last iteration re-reads its own unit: cached, unused).
+    const Meta nxt = meta_of(u + G < total ? u + G : u);
+    load_a(nxt, nbuf, nscale);
+    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before any MFMA
+
+    f32x4 acc[NRB][MT];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (W4) {
+#pragma unroll
+        for (int i = 0; i < AW; ++i) {
+          const float sv = bf16_bits_to_f32(ascale[rb][i]);
+          const float nsv = -24.f * sv;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const u32x4 af = w4_decode8(abuf[rb][i][j], sv, nsv);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(af, bfr[mt][i * 4 + j], acc[rb][mt]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < SPW; ++i)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(abuf[rb][i], bfr[mt][i], acc[rb][mt]);
+      }
+    }
+
+    f32x4 *red = s_red + (size_t)buf * kWaves * NRB * MT * kWave;
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((wave * NRB + rb) * MT + mt) * kWave + lane] = acc[rb][mt];
+
+    load_b(nxt);  // cur's B registers are free now
+    lds_barrier();
+
+    // Epilogue of cur: fixed-order sum of the eight K-slices.
+    if (KIND == 0) {
+      if (tid < MT * kWave) {
+        const int mt = tid >> 6, l = tid & 63;
+        const int j = mt * 16 + (l & 15);
+        f32x4 sg = red[(0 * MT + mt) * kWave + l];
+        f32x4 su = red[(1 * MT + mt) * kWave + l];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+          sg += red[((w * NRB + 0) * MT + mt) * kWave + l];
+          su += red[((w * NRB + 1) * MT + mt) * kWave + l];
+        }
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gt = bf16_round(sg[i]);
+          const float up = bf16_round(su[i]);
+          v[i] = gt / (1.0f + expf(-gt)) * up;
+        }
+        u32x2 packed;
+        packed[0] = pack_bf16x2(v[0], v[1]);
+        packed[1] = pack_bf16x2(v[2], v[3]);
+        if (j < cur.rows)
+          *(u32x2 *)(a.act + (size_t)(cur.row0 + j) * I + cur.cb * 16 + 4 * (l >> 4)) = packed;
+      }
+    } else {
+      if (tid < NRB * MT * kWave) {
+        const int rb = tid / (MT * kWave);
+        const int mt = (tid >> 6) % MT, l = tid & 63;
+        const int j = mt * 16 + (l & 15);
+        f32x4 sm = red[(rb * MT + mt) * kWave + l];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) sm += red[((w * NRB + rb) * MT + mt) * kWave + l];
+        const int q = __shfl(cur.idxv, j, kWave);
+        u32x2 packed;
+        packed[0] = pack_bf16x2(sm[0], sm[1]);
+        packed[1] = pack_bf16x2(sm[2], sm[3]);
+        if (j < cur.rows)
+          *(u32x2 *)(a.routed + (size_t)q * H + cur.cb * 32 + rb * 16 + 4 * (l >> 4)) = packed;
+      }
+    }
+
+    cur = nxt;
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+      for (int i = 0; i < AW; ++i) {
+        abuf[rb][i] = nbuf[rb][i];
+        ascale[rb][i] = nscale[rb][i];
+      }
+    buf ^= 1;
+  }
+}
+
+template <int KIND, int MT, int SPW, bool W4>
+hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
+  auto k = stream_kernel<KIND, MT, SPW, W4>;
+  const size_t lds = (size_t)2 * kWaves * 2 * MT * kWave * sizeof(f32x4);
+  static int per_cu = [&] {
+    int n = 1;
+    (void)hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kMaxLds);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k, kThreads, lds) !=
+            hipSuccess || n < 1)
+      n = 1;
+    return n;
+  }();
+  int grid = num_cus * per_cu;
+  if (grid > units_bound) grid = units_bound;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, s, a);
+  return hipGetLastError();
+}
+
+template <int KIND, int MT, bool W4>
+hipError_t launch_spw(const ExpertArgs &a, int spw, int units, int num_cus, hipStream_t s) {
+  if constexpr (W4) {
+    switch (spw) {
+      case 4: return launch_one<KIND, MT, 4, true>(a, units, num_cus, s);
+      case 8: return launch_one<KIND, MT, 8, true>(a, units, num_cus, s);
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (spw) {
+      case 1: return launch_one<KIND, MT, 1, false>(a, units, num_cus, s);
+      case 2: return launch_one<KIND, MT, 2, false>(a, units, num_cus, s);
+      case 3: return launch_one<KIND, MT, 3, false>(a, units, num_cus, s);
+      case 4: return launch_one<KIND, MT, 4, false>(a, units, num_cus, s);
+      case 6: return launch_one<KIND, MT, 6, false>(a, units, num_cus, s);
+      case 8: return launch_one<KIND, MT, 8, false>(a, units, num_cus, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+}
+
+bool spw_ok(int dim, bool w4) {
+  if (dim % 256) return false;
+  const int spw = dim / 256;
+  if (w4) return spw == 4 || spw == 8;
+  return spw == 1 || spw == 2 || spw == 3 || spw == 4 || spw == 6 || spw == 8;
+}
+
+}  // namespace
+
+bool stream_shape_ok(int H, int I, bool w4) { return spw_ok(H, w4) && spw_ok(I, false); }
+
+hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
+                                 int num_cus, hipStream_t s) {
+  const int units = task_capacity * (a.I / 16);
+  const int spw = a.H / 256;
+  if (token_block == 16)
+    return w4 ? launch_spw<0, 1, true>(a, spw, units, num_cus, s)
+              : launch_spw<0, 1, false>(a, spw, units, num_cus, s);
+  return w4 ? launch_spw<0, 2, true>(a, spw, units, num_cus, s)
+            : launch_spw<0, 2, false>(a, spw, units, num_cus, s);
+}
+
+hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,
+                              int num_cus, hipStream_t s) {
+  const int units = task_capacity * (a.H / 32);
+  const int spw = a.I / 256;
+  if (token_block == 16) return launch_spw<1, 1, false>(a, spw, units, num_cus, s);
+  return launch_spw<1, 2, false>(a, spw, units, num_cus, s);
+}
+
+}  // namespace moe

@@ -34,9 +34,9 @@ def test_library_exports_every_declared_function():
 
 
 def test_struct_sizes_match_header():
-    # 10 int32 + 10 pointers + size_t; 11 size_t + 4 int32.
+    # 10 int32 + 10 pointers + size_t; 13 size_t + 4 int32.
     assert ctypes.sizeof(N.MoeDesc) == 40 + 8 * 10 + 8
-    assert ctypes.sizeof(N.MoeLayout) == 8 * 11 + 16
+    assert ctypes.sizeof(N.MoeLayout) == 8 * 13 + 16
 
 
 def _desc(**kw):
@@ -70,6 +70,8 @@ def test_layout_for_qwen_shape():
     assert rc == 0 and lay.launches == 0
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=1024))
     assert lay.launches == 5
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=193))
+    assert lay.launches == 5
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17))
     assert lay.launches == 4
     rc, lay = _layout(_desc(H=33, I=19, E=8, K=2))
@@ -80,7 +82,7 @@ def test_layout_for_qwen_shape():
                                 dict(I=-1), dict(T=-1), dict(fmt=7), dict(ids=9), dict(tb=8),
                                 dict(route=N.ROUTE_LOGITS, ids=N.IDS_INT64),
                                 dict(route=N.ROUTE_LOGITS, E=4, K=8),
-                                dict(fmt=N.WEIGHTS_W4G128, H=192),
+                                dict(fmt=N.WEIGHTS_W4G128, H=192), dict(fmt=N.WEIGHTS_W4G128, H=512, I=256),
                                 dict(T=2 ** 27, K=16)])
 def test_layout_rejects_invalid_descriptors(kw):
     rc, _ = _layout(_desc(**kw))
