@@ -61,7 +61,7 @@ typedef struct moe_desc {
   int32_t id_dtype;               /* MOE_IDS_*   (MOE_IDS_INT32 in logits mode)    */
   int32_t route_mode;             /* MOE_ROUTE_*                                   */
   int32_t renormalize;            /* logits mode: divide top-k weights by their sum */
-  int32_t token_block;            /* 0 = choose from shape; else 16 or 32 rows    */
+  int32_t token_block;            /* 0 = choose from shape; 16/32 (stream) or 64 (tile) */
   const void *x;                  /* [T, H] bf16                                   */
   const void *logits;             /* [T, E] fp32 (logits mode) or NULL             */
   void *ids;                      /* [T, K] int32/int64                            */
@@ -93,7 +93,8 @@ typedef struct moe_layout {
   int32_t task_capacity;
   int32_t token_block;
   int32_t launches;   /* kernel launches per forward (0 when T == 0)             */
-  int32_t fast_path;  /* 1: MFMA kernels; 0: generic kernels for unaligned shapes */
+  int32_t fast_path;  /* 0 generic kernels (unaligned shapes), 1 MFMA weight      
+                         streaming, 2 MFMA LDS-tiled (many rows per expert)     */
 } moe_layout;
 
 typedef struct moe_plan moe_plan;

@@ -39,16 +39,29 @@ constexpr int kFuseRouterTokens = 64;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Shape-only kernel policy (never route contents, so a captured graph stays
+// valid when IDs change): mean rows per expert R/E below 32 -> weight
+// streaming with 16- or 32-row tasks; otherwise LDS-tiled GEMMs with 64-row
+// tasks.  An explicit token_block (16/32 stream, 64 tile) overrides it.
 int choose_token_block(const moe_desc *d) {
-  if (d->token_block == 16 || d->token_block == 32) return d->token_block;
-  // Mean rows per expert: small -> 16-row tasks, otherwise 32.
+  if (d->token_block == 16 || d->token_block == 32 || d->token_block == 64)
+    return d->token_block;
   const long long r = (long long)d->T * d->K;
-  return r <= 16LL * d->E ? 16 : 32;
+  if (r <= 16LL * d->E) return 16;
+  if (r < 32LL * d->E) return 32;
+  return 64;
 }
 
-bool shape_fast(const moe_desc *d, int) {
-  return moe::stream_shape_ok(d->H, d->I, d->weight_format == MOE_WEIGHTS_W4G128);
+int choose_path(const moe_desc *d, int tb) {
+  const bool w4 = d->weight_format == MOE_WEIGHTS_W4G128;
+  if (tb == 64) {
+    if (moe::tile_shape_ok(d->H, d->I, w4)) return moe::kTile;
+    return moe::stream_shape_ok(d->H, d->I, w4) ? moe::kStream : moe::kGeneric;
+  }
+  return moe::stream_shape_ok(d->H, d->I, w4) ? moe::kStream : moe::kGeneric;
 }
+
+bool shape_fast(const moe_desc *d, int tb) { return choose_path(d, tb) != moe::kGeneric; }
 
 int validate(const moe_desc *d) {
   if (!d) return fail(MOE_EINVAL, "null descriptor");
@@ -70,8 +83,9 @@ int validate(const moe_desc *d) {
     if (d->id_dtype != MOE_IDS_INT32) return fail(MOE_EINVAL, "router mode writes int32 ids");
     if (d->K > d->E) return fail(MOE_EINVAL, "top-k %d exceeds E %d", d->K, d->E);
   }
-  if (d->token_block != 0 && d->token_block != 16 && d->token_block != 32)
-    return fail(MOE_EINVAL, "token_block must be 0, 16 or 32");
+  if (d->token_block != 0 && d->token_block != 16 && d->token_block != 32 &&
+      d->token_block != 64)
+    return fail(MOE_EINVAL, "token_block must be 0, 16, 32 or 64");
   if (d->weight_format == MOE_WEIGHTS_W4G128) {
     if (!shape_fast(d, choose_token_block(d)))
       return fail(MOE_EINVAL, "W4G128 needs H %% 1024 == 0, I %% 256 == 0, H, I <= 4096");
@@ -107,7 +121,7 @@ moe_layout compute_layout(const moe_desc *d) {
   L.task_capacity = (int32_t)cap;
   L.token_block = tb;
   const bool fuse = d->route_mode == MOE_ROUTE_LOGITS && d->T <= kFuseRouterTokens;
-  L.fast_path = shape_fast(d, tb) ? 1 : 0;
+  L.fast_path = choose_path(d, tb);
   if (d->T == 0)
     L.launches = 0;
   else
@@ -123,7 +137,7 @@ struct moe_plan {
   int device;
   int num_cus;
   bool fuse_router;
-  bool fast;
+  int path;
 };
 
 extern "C" {
@@ -160,19 +174,23 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
     if (d->workspace_bytes < L.total)
       return fail(MOE_ESPACE, "workspace has %zu bytes, needs %zu", d->workspace_bytes, L.total);
   }
-  bool fast = L.fast_path != 0;
+  int path = L.fast_path;
+  // A stream-sized task block on a shape only the tiled kernels take (or the
+  // reverse) cannot happen: choose_path already matched them.
+  bool fast = path != moe::kGeneric;
   if (fast && !(aligned16(d->x) && aligned16(d->down) && aligned16(d->out) &&
                 (d->weight_format == MOE_WEIGHTS_W4G128 ? aligned16(d->w4_words)
                                                         : aligned16(d->gate_up))))
     fast = false;
+  if (!fast) path = moe::kGeneric;
   if (!fast && d->weight_format == MOE_WEIGHTS_W4G128)
     return fail(MOE_EINVAL, "W4G128 buffers must be 16-byte aligned");
   moe_plan *p = new (std::nothrow) moe_plan;
   if (!p) return fail(MOE_EINVAL, "out of host memory");
   p->d = *d;
   p->L = L;
-  p->L.fast_path = fast ? 1 : 0;
-  p->fast = fast;
+  p->L.fast_path = path;
+  p->path = path;
   p->fuse_router = d->route_mode == MOE_ROUTE_LOGITS && d->T <= kFuseRouterTokens;
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess)
@@ -261,10 +279,10 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
       case 0: e = moe::launch_router(ra, s); break;
       case 1: e = moe::launch_route_plan(ra, s); break;
       case 2:
-        e = moe::launch_gate_up(xa, L.task_capacity, L.token_block, w4, p->fast, p->num_cus, s);
+        e = moe::launch_gate_up(xa, L.task_capacity, L.token_block, w4, p->path, p->num_cus, s);
         break;
       case 3:
-        e = moe::launch_down(xa, L.task_capacity, L.token_block, p->fast, p->num_cus, s);
+        e = moe::launch_down(xa, L.task_capacity, L.token_block, p->path, p->num_cus, s);
         break;
       default: e = moe::launch_combine(xa, s); break;
     }

@@ -126,17 +126,19 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(const uint32_t *__restr
 }  // namespace
 
 hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
-                          bool fast, int num_cus, hipStream_t s) {
-  if (fast) return launch_stream_gate_up(a, task_capacity, token_block, w4, num_cus, s);
+                          int path, int num_cus, hipStream_t s) {
+  if (path == kTile) return launch_tile_gate_up(a, task_capacity, w4, num_cus, s);
+  if (path == kStream) return launch_stream_gate_up(a, task_capacity, token_block, w4, num_cus, s);
   if (w4) return hipErrorInvalidValue;
   const dim3 grid(task_capacity, (token_block * a.I + 255) / 256);
   hipLaunchKernelGGL(gate_up_generic_kernel, grid, dim3(256), 0, s, a, token_block);
   return hipGetLastError();
 }
 
-hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, bool fast,
+hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, int path,
                        int num_cus, hipStream_t s) {
-  if (fast) return launch_stream_down(a, task_capacity, token_block, num_cus, s);
+  if (path == kTile) return launch_tile_down(a, task_capacity, num_cus, s);
+  if (path == kStream) return launch_stream_down(a, task_capacity, token_block, num_cus, s);
   const dim3 grid(task_capacity, (token_block * a.H + 255) / 256);
   hipLaunchKernelGGL(down_generic_kernel, grid, dim3(256), 0, s, a, token_block);
   return hipGetLastError();

@@ -47,14 +47,21 @@ hipError_t launch_route_plan(const RouteArgs &a, hipStream_t s);
 // token_block: 16 or 32 grouped rows per task.  fast: MFMA kernels (shape
 // constraints checked by the caller), otherwise the generic kernels.
 hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
-                          bool fast, int num_cus, hipStream_t s);
-hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, bool fast,
+                          int path, int num_cus, hipStream_t s);
+hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, int path,
                        int num_cus, hipStream_t s);
 hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
                                  int num_cus, hipStream_t s);
 hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,
                               int num_cus, hipStream_t s);
 bool stream_shape_ok(int H, int I, bool w4);
+hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, bool w4, int num_cus,
+                               hipStream_t s);
+hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s);
+bool tile_shape_ok(int H, int I, bool w4);
+
+// Expert-stage kernel families (moe_layout.fast_path).
+enum Path { kGeneric = 0, kStream = 1, kTile = 2 };
 hipError_t launch_combine(const ExpertArgs &a, hipStream_t s);
 hipError_t launch_w4_dequantize(const uint32_t *words_t, const uint16_t *scales_t, int E, int N,
                                 int K, uint16_t *out, hipStream_t s);

@@ -1,0 +1,298 @@
+// LDS-tiled grouped GEMMs of the MoE forward on gfx950 for large row counts.
+//
+// When experts receive many rows (T = 1024, Zipf-skewed routing: a few
+// experts take ~1000 rows), streaming each weight byte once per 16/32-row task
+// would re-read the hot experts' weights dozens of times.  Here a task holds
+// up to BM = 64 grouped rows and a work unit is (task, n-tile of BN weight
+// rows); units are numbered n-tile-major so the consecutive tasks of one
+// expert share a weight tile, and consecutive units land on workgroups of the
+// same XCD, whose L2 then serves the repeated weight tile.
+//
+// Per unit: a K loop over BK-wide stages.  Each stage's weight tile [BN][BK]
+// and token tile [BM][BK] are loaded global -> registers (two stages in
+// flight) -> LDS, 16-byte chunks XOR-swizzled by row so that the MFMA
+// operand reads are bank-conflict free, then 8 waves (4 along N x 2 along M)
+// run 16x16x32 bf16 MFMAs.  W4G128 weights are decoded once into the bf16 LDS
+// tile with w4_decode8 (bit-exact dequantisation) and reused by all BM rows.
+//
+// Epilogues match the streaming kernels: gate/up round to bf16, SwiGLU in
+// fp32, bf16 act rows; down rounds to bf16 and scatters rows to route order.
+#include "common.h"
+#include "moe_internal.h"
+
+#define MOE_CONST __attribute__((address_space(4)))
+
+namespace moe {
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
+constexpr int BM = 64;
+
+template <typename T>
+__device__ __forceinline__ const MOE_CONST T *as_const(const T *p) {
+  return (const MOE_CONST T *)p;
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Byte offset of 16-byte chunk c of row `row` in a [rows][BK] bf16 tile.
+template <int BK>
+__device__ __forceinline__ int swz(int row, int c) {
+  if constexpr (BK == 64) return row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
+  else return row * 256 + ((c ^ (row & 15)) << 4);
+}
+
+template <int KIND, bool W4>
+struct TileCfg {
+  static constexpr int BN = (KIND == 0 && W4) ? 128 : 256;  // weight rows per tile
+  static constexpr int BK = W4 ? 128 : 64;
+  static constexpr int WNT = BN / 4 / 16;                   // 16-row tiles per wave
+  static constexpr int A_BYTES = BN * BK * 2;
+  static constexpr int B_BYTES = BM * BK * 2;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int A_LOADS = W4 ? 1 : A_BYTES / 1024 / kWaves;  // 16-B loads per lane
+  static constexpr int B_LOADS = B_BYTES / 1024 / kWaves;
+  static constexpr int OUT_COLS = KIND == 0 ? BN / 2 : BN;  // output columns per n-tile
+};
+
+template <int KIND, bool W4>
+__global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
+  using C = TileCfg<KIND, W4>;
+  constexpr int BN = C::BN, BK = C::BK, WNT = C::WNT;
+  constexpr int KS = BK / 32;  // MFMA k-steps per stage
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wn = wave & 3, wm = wave >> 2;
+  const int H = a.H, I = a.I;
+  const int Kdim = KIND == 0 ? H : I;
+  const int KT = Kdim / BK;  // even, >= 2 (checked on the host)
+  const int ntiles = (KIND == 0 ? I : H) / C::OUT_COLS;
+  const int num_tasks = *as_const(a.num_tasks);
+  const int total = num_tasks * ntiles;
+  const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
+
+  // XCD-aware slot: the first-wave dispatch places workgroup b on XCD b % 8,
+  // so slot numbers run contiguously within an XCD.
+  const int G = gridDim.x;
+  const int slot = (G % 8) ? (int)blockIdx.x : (int)(blockIdx.x / 8 + (blockIdx.x % 8) * (G / 8));
+
+  for (int u = slot; u < total; u += G) {
+    const int nt = u / num_tasks;
+    const int t = u - nt * num_tasks;
+    const int e = tasks[4 * t], row0 = tasks[4 * t + 1], rows = tasks[4 * t + 2];
+
+    // --- per-lane global sources of this unit -------------------------------
+    // Token tile rows: bf16 path rows = 8 per 1 KB load (64-K), W4 path 4 (128-K).
+    constexpr int B_RPL = 1024 / (BK * 2);  // rows per 1 KB
+    const uint16_t *bsrc[C::B_LOADS];
+    int brow[C::B_LOADS];
+#pragma unroll
+    for (int i = 0; i < C::B_LOADS; ++i) {
+      const int row = (wave * C::B_LOADS + i) * B_RPL + lane / (BK / 8);
+      brow[i] = row;
+      const int rr = row < rows ? row : 0;
+      size_t off;
+      if (KIND == 0) off = (size_t)a.row_token[row0 + rr] * H;
+      else off = (size_t)(row0 + rr) * I;
+      bsrc[i] = (KIND == 0 ? a.x : a.act) + off + (lane % (BK / 8)) * 8;
+    }
+    const uint16_t *asrc[C::A_LOADS];
+    int arow[C::A_LOADS];
+    const u32x4 *wsrc = nullptr;
+    const uint16_t *ssrc = nullptr;
+    if constexpr (W4) {
+      // Wave w decodes row block w (16 rows) of the 128-row tile.
+      const int G4 = H >> 7;
+      const int half = wave >> 2;  // 0: gate rows, 1: up rows
+      const size_t rb = (size_t)e * (2 * I / 16) + (half ? I / 16 : 0) + (nt * 64 + (wave & 3) * 16) / 16;
+      wsrc = (const u32x4 *)a.w4_words + rb * G4 * 64 + lane;
+      ssrc = a.w4_scales + rb * G4 * 16 + (lane & 15);
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::A_LOADS; ++i) {
+        const int row = (wave * C::A_LOADS + i) * 8 + lane / 8;  // tile row
+        arow[i] = row;
+        size_t wrow;
+        if (KIND == 0)
+          wrow = (size_t)e * 2 * I + (row < BN / 2 ? nt * (BN / 2) + row : I + nt * (BN / 2) + row - BN / 2);
+        else
+          wrow = (size_t)e * H + nt * BN + row;
+        asrc[i] = (KIND == 0 ? a.gate_up : a.down) + wrow * Kdim + (lane % 8) * 8;
+      }
+    }
+
+    // --- register stage sets ---------------------------------------------
+    struct Regs {
+      u32x4 a[W4 ? 1 : C::A_LOADS];
+      uint32_t s;
+      u32x4 b[C::B_LOADS];
+    };
+    auto gload = [&](Regs &R, int kt) {
+      if constexpr (W4) {
+        R.a[0] = wsrc[(size_t)kt * 64];
+        R.s = ssrc[kt * 16];
+      } else {
+#pragma unroll
+        for (int i = 0; i < C::A_LOADS; ++i) R.a[i] = *(const u32x4 *)(asrc[i] + kt * BK);
+      }
+#pragma unroll
+      for (int i = 0; i < C::B_LOADS; ++i) R.b[i] = *(const u32x4 *)(bsrc[i] + kt * BK);
+    };
+    auto sts = [&](uint8_t *buf, const Regs &R) {
+      uint8_t *abuf = buf, *bbuf = buf + C::A_BYTES;
+      if constexpr (W4) {
+        const float sv = bf16_bits_to_f32(R.s);
+        const float nsv = -24.f * sv;
+        const int row = wave * 16 + (lane & 15);
+        const int g = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *(u32x4 *)(abuf + swz<BK>(row, 4 * j + g)) = w4_decode8(R.a[0][j], sv, nsv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < C::A_LOADS; ++i) *(u32x4 *)(abuf + swz<BK>(arow[i], lane % 8)) = R.a[i];
+      }
+#pragma unroll
+      for (int i = 0; i < C::B_LOADS; ++i)
+        *(u32x4 *)(bbuf + swz<BK>(brow[i], lane % (BK / 8))) = R.b[i];
+    };
+
+    // --- MFMA on one LDS stage ------------------------------------------------
+    // Wave (wn, wm): weight row tiles (gate/up: wn's slice of both halves),
+    // token tiles wm*32 + {0, 16}.  Lane l reads row l%16, chunk 4*ks + l/16.
+    f32x4 acc[WNT][2];
+#pragma unroll
+    for (int i = 0; i < WNT; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto a_row = [&](int i) {
+      if (KIND == 0) {
+        constexpr int HALF_T = WNT / 2;  // tiles per half per wave
+        return (i < HALF_T ? 0 : BN / 2) + wn * HALF_T * 16 + (i % HALF_T) * 16;
+      }
+      return wn * WNT * 16 + i * 16;
+    };
+    auto compute = [&](const uint8_t *buf) {
+      const uint8_t *abuf = buf, *bbuf = buf + C::A_BYTES;
+      const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int c = 4 * ks + g;
+        const u32x4 b0 = *(const u32x4 *)(bbuf + swz<BK>(wm * 32 + r, c));
+        const u32x4 b1 = *(const u32x4 *)(bbuf + swz<BK>(wm * 32 + 16 + r, c));
+#pragma unroll
+        for (int i = 0; i < WNT; ++i) {
+          const u32x4 af = *(const u32x4 *)(abuf + swz<BK>(a_row(i) + r, c));
+          acc[i][0] = mfma16(af, b0, acc[i][0]);
+          acc[i][1] = mfma16(af, b1, acc[i][1]);
+        }
+      }
+    };
+
+    uint8_t *buf0 = smem, *buf1 = smem + C::STAGE_BYTES;
+    Regs R0, R1;
+    gload(R0, 0);
+    gload(R1, 1);
+    sts(buf0, R0);
+    gload(R0, 2 < KT ? 2 : KT - 1);
+    lds_barrier();
+    for (int kt = 0; kt < KT; kt += 2) {
+      compute(buf0);
+      sts(buf1, R1);  // stage kt+1
+      gload(R1, kt + 3 < KT ? kt + 3 : KT - 1);
+      lds_barrier();
+      compute(buf1);
+      sts(buf0, R0);  // stage kt+2 (a harmless copy of the last stage at the end)
+      gload(R0, kt + 4 < KT ? kt + 4 : KT - 1);
+      lds_barrier();
+    }
+
+    // --- epilogue: lane holds rows 4*(l/16)+i of its 16-row tile, token l%16 --
+    const int g = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int tok = wm * 32 + mt * 16 + (lane & 15);
+      if (KIND == 0) {
+        constexpr int HALF_T = WNT / 2;
+#pragma unroll
+        for (int i = 0; i < HALF_T; ++i) {
+          const f32x4 sg = acc[i][mt], su = acc[i + HALF_T][mt];
+          float v[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float gt = bf16_round(sg[k]);
+            const float up = bf16_round(su[k]);
+            v[k] = gt / (1.0f + expf(-gt)) * up;
+          }
+          u32x2 packed;
+          packed[0] = pack_bf16x2(v[0], v[1]);
+          packed[1] = pack_bf16x2(v[2], v[3]);
+          const int col = nt * (BN / 2) + wn * HALF_T * 16 + i * 16 + 4 * g;
+          if (tok < rows) *(u32x2 *)(a.act + (size_t)(row0 + tok) * I + col) = packed;
+        }
+      } else {
+        const int q = tok < rows ? a.row_route[row0 + tok] : 0;
+#pragma unroll
+        for (int i = 0; i < WNT; ++i) {
+          u32x2 packed;
+          packed[0] = pack_bf16x2(acc[i][mt][0], acc[i][mt][1]);
+          packed[1] = pack_bf16x2(acc[i][mt][2], acc[i][mt][3]);
+          const int col = nt * BN + wn * WNT * 16 + i * 16 + 4 * g;
+          if (tok < rows) *(u32x2 *)(a.routed + (size_t)q * H + col) = packed;
+        }
+      }
+    }
+    lds_barrier();  // the next unit's prologue rewrites buf0
+  }
+}
+
+template <int KIND, bool W4>
+hipError_t launch_tile_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
+  using C = TileCfg<KIND, W4>;
+  auto k = tile_kernel<KIND, W4>;
+  const size_t lds = 2 * (size_t)C::STAGE_BYTES;
+  static int per_cu = [&] {
+    int n = 1;
+    (void)hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kMaxLds);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k, kThreads, lds) !=
+            hipSuccess || n < 1)
+      n = 1;
+    return n;
+  }();
+  int grid = num_cus * per_cu;
+  if (grid > units_bound) grid = units_bound;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool tile_shape_ok(int H, int I, bool w4) {
+  // gate/up: K = H in BK stages (even count), act columns in BN/2 tiles;
+  // down: K = I in 64-wide stages (even count), H in 256-row tiles.
+  const int bk_gu = w4 ? 128 : 64;
+  if (H % (2 * bk_gu) || I % 128) return false;
+  if (I % (w4 ? 64 : 128)) return false;
+  if (H % 256) return false;
+  return true;
+}
+
+hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, bool w4, int num_cus,
+                               hipStream_t s) {
+  if (w4) return launch_tile_one<0, true>(a, task_capacity * (a.I / 64), num_cus, s);
+  return launch_tile_one<0, false>(a, task_capacity * (a.I / 128), num_cus, s);
+}
+
+hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
+  return launch_tile_one<1, false>(a, task_capacity * (a.H / 256), num_cus, s);
+}
+
+}  // namespace moe

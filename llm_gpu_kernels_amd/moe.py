@@ -38,8 +38,10 @@ _CREATE_LOCK = threading.Lock()
 @dataclass(frozen=True)
 class GemmConfig:
     """Tile choice (reference gemm.py:13-25).  Only ``block_m`` (grouped rows
-    per task: 16 or 32) is meaningful on gfx950; the column tiles and the
-    K-pipeline depth are fixed by the kernels' wave layout."""
+    per task) is meaningful on gfx950: 16 or 32 select the weight-streaming
+    kernels, 64 the LDS-tiled kernels; 0 lets the shape policy choose.  The
+    column tiles and the K-pipeline depth are fixed by the kernels' wave
+    layout."""
     block_m: int = 0
     block_n: int = 0
     block_k: int = 0
@@ -60,7 +62,9 @@ class FrozenMoEPolicy:
         mu = tokens * topk / max(experts, 1)
         if mu <= self.small_mu:
             return GemmConfig(block_m=16), "small"
-        return GemmConfig(block_m=32), "large"
+        if mu < 2 * self.small_mu:
+            return GemmConfig(block_m=32), "medium"
+        return GemmConfig(block_m=64), "large"
 
 
 def _device_check(tensors, device):
@@ -117,7 +121,7 @@ class PreparedMoE:
         d.id_dtype = N.IDS_INT64 if ids.dtype == torch.int64 else N.IDS_INT32
         d.route_mode = N.ROUTE_LOGITS if logits is not None else N.ROUTE_FIXED
         d.renormalize = 1 if renormalize else 0
-        d.token_block = self.config.block_m if self.config.block_m in (16, 32) else 0
+        d.token_block = self.config.block_m if self.config.block_m in (16, 32, 64) else 0
         lay = N.MoeLayout()
         N.check(N.lib().moe_workspace_layout(ctypes.byref(d), ctypes.byref(lay)), "prepare")
         # Zero-initialised: the router flag word is self-clearing from then on.

@@ -65,7 +65,9 @@ def test_layout_for_qwen_shape():
     assert lay.act % 256 == 0 and lay.routed % 256 == 0
     assert lay.total >= lay.routed + r * 2048 * 2
     rc, lay = _layout(_desc(T=1024))
-    assert lay.token_block == 32
+    assert lay.token_block == 64 and lay.fast_path == 2
+    rc, lay = _layout(_desc(T=300))
+    assert lay.token_block == 32 and lay.fast_path == 1
     rc, lay = _layout(_desc(T=0))
     assert rc == 0 and lay.launches == 0
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=1024))
@@ -79,7 +81,7 @@ def test_layout_for_qwen_shape():
 
 
 @pytest.mark.parametrize("kw", [dict(E=0), dict(E=257), dict(K=0), dict(K=33), dict(H=0),
-                                dict(I=-1), dict(T=-1), dict(fmt=7), dict(ids=9), dict(tb=8),
+                                dict(I=-1), dict(T=-1), dict(fmt=7), dict(ids=9), dict(tb=8), dict(tb=48),
                                 dict(route=N.ROUTE_LOGITS, ids=N.IDS_INT64),
                                 dict(route=N.ROUTE_LOGITS, E=4, K=8),
                                 dict(fmt=N.WEIGHTS_W4G128, H=192), dict(fmt=N.WEIGHTS_W4G128, H=512, I=256),

@@ -74,16 +74,40 @@ def test_reference_functional_specs(case, gpu_device):
     assert ms["passed"], ms
 
 
-@pytest.mark.parametrize("block", [16, 32])
-def test_token_block_invariance(block, gpu_device):
-    """Each grouped row's arithmetic is independent of the task size: bitwise equal."""
+def test_token_block_invariance(gpu_device):
+    """Streaming kernels: each grouped row's arithmetic is independent of the
+    task size (16 or 32 rows), so the outputs are bitwise equal."""
     lay = make_layer("qwen", 193, seed=3, device=gpu_device)
     ids, w = O.route_topk(lay["logits"].cpu(), 8)
     args = (lay["x"], lay["gate_up"], lay["down"], ids.to(gpu_device), w.to(gpu_device))
-    a = prepare_moe(*args, config=GemmConfig(block_m=block)).run().clone()
-    b = prepare_moe(*args, config=GemmConfig(block_m=48 - block)).run().clone()
+    pa = prepare_moe(*args, config=GemmConfig(block_m=16))
+    pb = prepare_moe(*args, config=GemmConfig(block_m=32))
+    assert pa.layout.fast_path == 1 and pb.layout.fast_path == 1
+    a, b = pa.run().clone(), pb.run().clone()
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens,w4", [(17, False), (193, False), (193, True)])
+def test_tiled_path_forced(tokens, w4, gpu_device):
+    """LDS-tiled kernels (64-row tasks) on small T: partial tiles and tail rows."""
+    lay = make_layer("qwen", tokens, seed=4, device=gpu_device)
+    ids, w = O.route_topk(lay["logits"].cpu(), 8)
+    gate_up, ref_gu = lay["gate_up"], lay["gate_up"].cpu()
+    if w4:
+        packed = quantize_gate_up(ref_gu)
+        gate_up = tile_gate_up(packed).to(gpu_device)
+        ref_gu = O.dequantize_w4(packed.words, packed.scales)
+        plan = prepare_w4_moe(lay["x"], gate_up, lay["down"], ids.to(gpu_device), w.to(gpu_device),
+                              down_config=GemmConfig(block_m=64))
+    else:
+        plan = prepare_moe(lay["x"], gate_up, lay["down"], ids.to(gpu_device), w.to(gpu_device),
+                           config=GemmConfig(block_m=64))
+    assert plan.layout.fast_path == 2
+    out = plan.run()
+    torch.cuda.synchronize()
+    m = O.error(out, O.moe_reference(lay["x"].cpu(), ref_gu, lay["down"].cpu(), ids, w))
+    assert m["passed"], m
 
 
 CONFIGS = [("tiny", 17, "uniform"), ("qwen", 17, "uniform"), ("qwen", 193, "uniform"),
@@ -106,6 +130,8 @@ def _routed_parity(shape, tokens, routing, gpu_device, w4=False):
     else:
         weights_for_oracle = gate_up.cpu()
     plan = prepare_routed_moe(lay["x"], lay["logits"], gate_up, lay["down"], k)
+    expect_path = 2 if tokens * k >= 32 * lay["E"] else 1
+    assert plan.layout.fast_path == expect_path
     out = plan.forward(lay["x"], lay["logits"])
     torch.cuda.synchronize()
     plan.check_inputs()
