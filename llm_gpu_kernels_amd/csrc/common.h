@@ -27,12 +27,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 with gfx950's v_cvt_pk_bf16_f32 (IEEE
+// round-to-nearest-even, identical to f32_to_bf16_bits for every non-NaN).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ float bf16_round(float f) {
-  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+  return bf16_bits_to_f32(pack_bf16x2(f, 0.f) & 0xffffu);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
@@ -68,24 +74,53 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-// Decode one packed word of eight int4 values (nibble = q + 8, earliest K in
-// the low nibble) into eight bf16 values bf16_rn(q * scale), packed in pairs.
-// 16 + n is built exactly as a float (n in mantissa bits 22..19), and
-// fma(16 + n, s, -24 s) = (n - 8) s is exact (<= 13 significant bits), so the
-// only rounding is the final bf16 conversion -- identical to rounding the
-// exact product float(q) * float(scale).
-__device__ __forceinline__ u32x4 w4_decode8(uint32_t w, float s, float neg24s) {
-  float f[8];
+// W4G128 decode: packed word of eight int4 (nibble = q + 8, earliest K in the
+// low nibble) -> eight bf16 values bf16_rn(q * scale), packed in pairs.
+//
+// Nibble n sitting at bits 4p..4p+3 (p = 2, 3, 4: inside the 23-bit mantissa)
+// of a word whose other bits are replaced by those of 2^23 (one v_bfi_b32)
+// reads as the float 2^23 + n * 16^p.  With per-group constants
+// sp = s * 16^-p and cp = -(2^(23-4p) + 8) * s (both exact: power-of-two
+// scaling, and an 8-bit-significand scale times an integer of at most 13
+// significant bits),
+//   fma(2^23 + n * 16^p, sp, cp) = (2^(23-4p) + n) s - (2^(23-4p) + 8) s
+//                                = (n - 8) s  exactly (<= 12 significant bits),
+// so the only rounding is the final bf16 conversion -- the same as rounding
+// float(q) * float(scale).  Nibbles 2..4 decode in place, nibbles 0..1 from
+// w << 8 and nibbles 5..7 from w >> 12.
+struct W4Scale {
+  float sp[3], cp[3];  // p = 2, 3, 4
+};
+
+__device__ __forceinline__ W4Scale w4_scale(float s) {
+  W4Scale k;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t nib = (w >> (4 * i)) & 0xfu;
-    f[i] = __builtin_fmaf(__uint_as_float(0x41800000u | (nib << 19)), s, neg24s);
+  for (int i = 0; i < 3; ++i) {
+    const int p = i + 2;
+    k.sp[i] = s * __uint_as_float((uint32_t)(127 - 4 * p) << 23);  // s * 2^-4p
+    k.cp[i] = -s * (float)((1 << (23 - 4 * p)) + 8);
   }
+  return k;
+}
+
+__device__ __forceinline__ uint32_t bfi_b32(uint32_t mask, uint32_t src, uint32_t other) {
+  uint32_t d;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(d) : "v"(mask), "v"(src), "v"(other));
+  return d;
+}
+
+__device__ __forceinline__ u32x4 w4_decode8(uint32_t w, const W4Scale &k) {
+  const uint32_t magic = 0x4b000000u;  // 2^23: exponent bits only, empty mantissa
+  const uint32_t lo = w << 8, hi = w >> 12;
+  auto dq = [&](uint32_t src, int p) {
+    return __builtin_fmaf(__uint_as_float(bfi_b32(0xfu << (4 * p), src, magic)), k.sp[p - 2],
+                          k.cp[p - 2]);
+  };
   u32x4 r;
-  r[0] = pack_bf16x2(f[0], f[1]);
-  r[1] = pack_bf16x2(f[2], f[3]);
-  r[2] = pack_bf16x2(f[4], f[5]);
-  r[3] = pack_bf16x2(f[6], f[7]);
+  r[0] = pack_bf16x2(dq(lo, 2), dq(lo, 3));  // nibbles 0, 1
+  r[1] = pack_bf16x2(dq(w, 2), dq(w, 3));    // nibbles 2, 3
+  r[2] = pack_bf16x2(dq(w, 4), dq(hi, 2));   // nibbles 4, 5
+  r[3] = pack_bf16x2(dq(hi, 3), dq(hi, 4));  // nibbles 6, 7
   return r;
 }
 

@@ -117,10 +117,10 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(const uint32_t *__restr
   const int rb = (int)(erb % (N / 16));
   const int r = lane & 15, g = lane >> 4;
   const u32x4 w = ((const u32x4 *)words_t)[i];
-  const float s = bf16_bits_to_f32(scales_t[ug * 16 + r]);
+  const W4Scale ks = w4_scale(bf16_bits_to_f32(scales_t[ug * 16 + r]));
   uint16_t *row = out + ((size_t)e * N + rb * 16 + r) * K + grp * 128 + g * 8;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) *(u32x4 *)(row + 32 * j) = w4_decode8(w[j], s, -24.f * s);
+  for (int j = 0; j < 4; ++j) *(u32x4 *)(row + 32 * j) = w4_decode8(w[j], ks);
 }
 
 }  // namespace

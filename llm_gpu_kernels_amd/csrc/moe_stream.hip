@@ -28,6 +28,8 @@
 //  * W4G128: the 16-byte load of a lane holds 32 int4 of one row (a whole
 //    128-K group, 4 MFMA k-steps) and is decoded in registers by
 //    w4_decode8, bit-exact with the reference dequantisation.
+#include <type_traits>
+
 #include "common.h"
 #include "moe_internal.h"
 
@@ -128,18 +130,24 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   };
 
   // A operand: bf16 -> [NRB][SPW] fragments; W4 -> [NRB][SPW/4] words + scales.
+  // A ring of S unit slots keeps S-1 units of weights in flight (W4 units are
+  // 4x smaller, so they need a deeper ring).  Slots are compile-time indices
+  // of an unrolled loop: copying a register whose load is still in flight
+  // would make the wave wait for it.
   constexpr int AW = W4 ? SPW / 4 : SPW;
-  u32x4 abuf[NRB][AW], nbuf[NRB][AW];
-  uint32_t ascale[NRB][AW], nscale[NRB][AW];
+  constexpr int S = W4 ? 4 : 2;
+  u32x4 aq[S][NRB][AW];
+  uint32_t sq[S][NRB][AW];
+  Meta mq[S];
   auto load_a = [&](const Meta &m, u32x4 (&buf)[NRB][AW], uint32_t (&sc)[NRB][AW]) {
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       if constexpr (W4) {
-        const int G = H >> 7;
+        const int G4 = H >> 7;
         const size_t rbi = (size_t)m.expert * (2 * I / 16) + m.cb + (rb ? I / 16 : 0);
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
-          const size_t unit = rbi * G + (s0 >> 2) + i;
+          const size_t unit = rbi * G4 + (s0 >> 2) + i;
           buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + lane];
           sc[rb][i] = a.w4_scales[unit * 16 + r];
         }
@@ -156,17 +164,20 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
     }
   };
 
-  Meta cur = meta_of(u_begin);
-  load_a(cur, abuf, ascale);
-  load_b(cur);
-  int buf = 0;
+  // Prologue: units u_begin + p*G (clamped to a valid unit) into slots p < S.
+#pragma unroll
+  for (int p = 0; p < S; ++p) {
+    const int up = u_begin + p * G;
+    mq[p] = meta_of(up < total ? up : u_begin);
+    load_a(mq[p], aq[p], sq[p]);
+  }
+  load_b(mq[0]);
 
-  for (int u = u_begin; u < total; u += G) {
-    // Next unit (the last iteration re-reads its own unit: cached, unused).
-    const Meta nxt = meta_of(u + G < total ? u + G : u);
-    load_a(nxt, nbuf, nscale);
-    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before any MFMA
-
+  int u = u_begin;
+  // One unit in ring slot SL; returns whether another unit follows.
+  auto step = [&](auto slot_tag) -> bool {
+    constexpr int SL = decltype(slot_tag)::value;
+    const Meta &cur = mq[SL];
     f32x4 acc[NRB][MT];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
@@ -175,11 +186,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
       if constexpr (W4) {
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
-          const float sv = bf16_bits_to_f32(ascale[rb][i]);
-          const float nsv = -24.f * sv;
+          const W4Scale ks = w4_scale(bf16_bits_to_f32(sq[SL][rb][i]));
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const u32x4 af = w4_decode8(abuf[rb][i][j], sv, nsv);
+            const u32x4 af = w4_decode8(aq[SL][rb][i][j], ks);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(af, bfr[mt][i * 4 + j], acc[rb][mt]);
           }
@@ -188,17 +198,17 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
 #pragma unroll
         for (int i = 0; i < SPW; ++i)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(abuf[rb][i], bfr[mt][i], acc[rb][mt]);
+          for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(aq[SL][rb][i], bfr[mt][i], acc[rb][mt]);
       }
     }
 
-    f32x4 *red = s_red + (size_t)buf * kWaves * NRB * MT * kWave;
+    f32x4 *red = s_red + (size_t)(SL & 1) * kWaves * NRB * MT * kWave;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) red[((wave * NRB + rb) * MT + mt) * kWave + lane] = acc[rb][mt];
 
-    load_b(nxt);  // cur's B registers are free now
+    load_b(mq[(SL + 1) % S]);  // cur's B registers are free now
     lds_barrier();
 
     // Epilogue of cur: fixed-order sum of the eight K-slices.
@@ -243,15 +253,23 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
       }
     }
 
-    cur = nxt;
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-      for (int i = 0; i < AW; ++i) {
-        abuf[rb][i] = nbuf[rb][i];
-        ascale[rb][i] = nscale[rb][i];
-      }
-    buf ^= 1;
+    // Refill this slot with the unit S positions ahead (clamped: a cached
+    // re-read of the current unit near the end).
+    const int uf = u + S * G;
+    mq[SL] = meta_of(uf < total ? uf : u);
+    load_a(mq[SL], aq[SL], sq[SL]);
+    u += G;
+    return u < total;
+  };
+
+  using std::integral_constant;
+  while (true) {
+    if (!step(integral_constant<int, 0>{})) break;
+    if (!step(integral_constant<int, 1>{})) break;
+    if constexpr (S == 4) {
+      if (!step(integral_constant<int, 2>{})) break;
+      if (!step(integral_constant<int, 3>{})) break;
+    }
   }
 }
 

@@ -149,13 +149,12 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
     auto sts = [&](uint8_t *buf, const Regs &R) {
       uint8_t *abuf = buf, *bbuf = buf + C::A_BYTES;
       if constexpr (W4) {
-        const float sv = bf16_bits_to_f32(R.s);
-        const float nsv = -24.f * sv;
+        const W4Scale ks = w4_scale(bf16_bits_to_f32(R.s));
         const int row = wave * 16 + (lane & 15);
         const int g = lane >> 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          *(u32x4 *)(abuf + swz<BK>(row, 4 * j + g)) = w4_decode8(R.a[0][j], sv, nsv);
+          *(u32x4 *)(abuf + swz<BK>(row, 4 * j + g)) = w4_decode8(R.a[0][j], ks);
       } else {
 #pragma unroll
         for (int i = 0; i < C::A_LOADS; ++i) *(u32x4 *)(abuf + swz<BK>(arow[i], lane % 8)) = R.a[i];

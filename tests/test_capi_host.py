@@ -138,29 +138,43 @@ def O_packed(words, scales):
     return PackedGateUp(words, scales, {})
 
 
+def _decode_word_like_kernel(word, s):
+    """Host restatement of the kernel's w4_decode8 (llm_gpu_kernels_amd/csrc/common.h):
+    nibble n at mantissa position p of 2^23 -> fma(2^23 + n*16^p, s*16^-p,
+    -(2^(23-4p)+8)*s), evaluated exactly in float64, rounded once to fp32."""
+    import struct
+    def fl(b):
+        return struct.unpack("<f", struct.pack("<I", b & 0xFFFFFFFF))[0]
+    lo, hi = (word << 8) & 0xFFFFFFFF, word >> 12
+    plan = [(lo, 2), (lo, 3), (word, 2), (word, 3), (word, 4), (hi, 2), (hi, 3), (hi, 4)]
+    out = []
+    for src, p in plan:
+        v = fl(0x4B000000 | (src & (0xF << (4 * p))))
+        sp = float(torch.tensor(s * 2.0 ** (-4 * p), dtype=torch.float32))
+        cp = float(torch.tensor(-s * float(2 ** (23 - 4 * p) + 8), dtype=torch.float32))
+        out.append(float(torch.tensor(v * sp + cp, dtype=torch.float32)))
+    return out
+
+
 def test_tile_emulated_decode_matches_oracle_dequant():
-    """Host emulation of the kernel's (16+n)*s - 24*s decode on the tiled layout."""
+    """Host emulation of the kernel decode on the tiled layout == oracle dequant."""
     g = torch.Generator().manual_seed(11)
-    w = (torch.randn((2, 32, 256), generator=g) * 0.03).to(torch.bfloat16)
+    w = (torch.randn((1, 32, 256), generator=g) * 0.03).to(torch.bfloat16)
+    w[0, 5, :128] = 0  # scale 1 group
     p = quantize_gate_up(w)
     t = tile_gate_up(p)
     ref = O.dequantize_w4(p.words, p.scales)
-    e, n, k = 2, 32, 256
+    e, n, k = 1, 32, 256
     out = torch.empty((e, n, k), dtype=torch.bfloat16)
     wt = t.words.to(torch.int64) & 0xFFFFFFFF
     st = t.scales.float()
-    for ei in range(e):
-        for rb in range(n // 16):
-            for grp in range(k // 128):
-                for lane in range(64):
-                    r, gg = lane % 16, lane // 16
-                    s = st[ei, rb, grp, r]
-                    for j in range(4):
-                        wd = int(wt[ei, rb, grp, lane, j])
-                        for i in range(8):
-                            nib = (wd >> (4 * i)) & 15
-                            f = torch.tensor(16.0 + nib, dtype=torch.float32)
-                            val = (f * s).double() - 24 * s.double()  # exact, as fma
-                            out[ei, rb * 16 + r, grp * 128 + 32 * j + 8 * gg + i] = \
-                                torch.tensor(float(val), dtype=torch.float32).to(torch.bfloat16)
+    for rb in range(n // 16):
+        for grp in range(k // 128):
+            for lane in range(64):
+                r, gg = lane % 16, lane // 16
+                s = float(st[0, rb, grp, r])
+                for j in range(4):
+                    vals = _decode_word_like_kernel(int(wt[0, rb, grp, lane, j]), s)
+                    base = grp * 128 + 32 * j + 8 * gg
+                    out[0, rb * 16 + r, base:base + 8] = torch.tensor(vals).to(torch.bfloat16)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
