@@ -181,6 +181,34 @@ def cpu_baseline(lay, spec, budget_s=12.0):
                       f"os.cpu_count()={os.cpu_count()})"}
 
 
+def copy_calibration(mib: int):
+    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE /
+    WRITE_SIZE readings (KiB per dispatch) into HBM bytes."""
+    n = mib * (1 << 20) // 2
+    src = torch.randn(n, device="cuda:0").to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 2, "copy_calibration_bytes_written": n * 2,
+                      "dispatches": 10}), flush=True)
+
+
+def profiled_traffic(workload: str):
+    """HBM bytes per gate/up launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"gate_up_traffic_{workload}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,7 +217,12 @@ def main():
     ap.add_argument("--workload", default="qwen-bf16-t17", choices=sorted(WORKLOADS))
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain MIB-MiB device copy 10 times (PMC scaling)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(one MI355X per box); run with --gpus 1", file=sys.stderr)
@@ -229,7 +262,8 @@ def main():
         "us_per_layer": main_res["us_per_layer"],
         "roofline": {"bound": "hbm", "kernel": "gate_up_swiglu", "achieved": gu["gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_us": gu["us"], "algorithmic_bytes": gu["bytes"]},
+                     "traffic": profiled_traffic(args.workload), "avg_us": gu["us"],
+                     "algorithmic_bytes": gu["bytes"]},
         "layer_roofline": {"bound": "hbm", "achieved": main_res["layer_hbm_gbs"],
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": main_res["layer_hbm_frac"]},
         "cpu_baseline": cpu,

@@ -33,9 +33,10 @@ int hip_fail(hipError_t e, const char *what) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Router fused into the planner's single workgroup (16 waves) up to this many
-// tokens; beyond it a separate one-wave-per-token launch is faster.
-constexpr int kFuseRouterTokens = 64;
+// Router fused into the planner's single workgroup up to one token per wave
+// (16); beyond that the standalone one-wave-per-token launch routes all
+// tokens in parallel across CUs, which is faster than further serial rounds.
+constexpr int kFuseRouterTokens = 16;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 

@@ -71,13 +71,17 @@ __device__ __forceinline__ float key_float(uint32_t k) {
 }
 
 // One wave routes token t.  Expert e lives in lane e % 64, slot e / 64.
-// Selection is by logit (softmax is monotone): K rounds of a wave max over
-// the remaining keys, then the lowest expert index holding that key, so the
-// top-k come out in slot order with ties to the lower index.  NaN logits
-// rank below every number and set the logit flag.
+// Selection is by logit (softmax is monotone): K rounds of a DPP wave max
+// over the remaining keys; the lowest expert holding the max is the first
+// set bit of the first non-empty per-slot ballot (slot j holds experts
+// 64j + lane), all scalar.  Lane k keeps the key and expert of slot k and
+// the probabilities are formed once, after the loop.  NaN logits rank below
+// every number and set the logit flag.  Results go to global memory and,
+// when `lds_ids` is given, to LDS for the planner.
 __device__ void route_token(const float *__restrict__ logits, int t, int E, int K,
                             int renormalize, int32_t *__restrict__ ids_out,
-                            float *__restrict__ w_out, uint32_t &flags) {
+                            float *__restrict__ w_out, uint32_t &flags, int *lds_ids,
+                            float *lds_w) {
   const int lane = threadIdx.x & (kWave - 1);
   float raw[4];
   uint32_t key[4];
@@ -86,11 +90,11 @@ __device__ void route_token(const float *__restrict__ logits, int t, int E, int 
   for (int j = 0; j < 4; ++j) {
     const int e = lane + kWave * j;
     raw[j] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
-    bad |= (e < E) && !isfinite(raw[j]);
+    bad |= e < E && !isfinite(raw[j]);
     key[j] = e < E ? float_key(raw[j]) : 0u;
   }
   if (__any(bad)) flags |= 4u;
-  uint32_t top = umax_(umax_(key[0], key[1]), umax_(key[2], key[3]));
+  const uint32_t top = umax_(umax_(key[0], key[1]), umax_(key[2], key[3]));
   const float m = key_float(wave_umax(top));
   float z = 0.f;
 #pragma unroll
@@ -98,8 +102,7 @@ __device__ void route_token(const float *__restrict__ logits, int t, int E, int 
     if (lane + kWave * j < E) z += expf(raw[j] - m);
   z = wave_fsum(z);
 
-  uint32_t taken = 0;
-  float my_p = 0.f, psum = 0.f;
+  uint32_t taken = 0, my_key = 0;
   int my_id = 0;
   for (int k = 0; k < K; ++k) {
     uint32_t best = 0;
@@ -107,24 +110,30 @@ __device__ void route_token(const float *__restrict__ logits, int t, int E, int 
     for (int j = 0; j < 4; ++j)
       if (!((taken >> j) & 1)) best = umax_(best, key[j]);
     const uint32_t M = wave_umax(best);
-    uint32_t cand = 0xffffu;
+    int idx = kMaxExperts;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = lane + kWave * j;
-      if (e < E && !((taken >> j) & 1) && key[j] == M) cand = umin_(cand, (uint32_t)e);
+    for (int j = 3; j >= 0; --j) {  // lowest slot wins: scan from the top down
+      const uint64_t hit = __ballot(lane + kWave * j < E && !((taken >> j) & 1) && key[j] == M);
+      idx = hit ? kWave * j + (int)__builtin_ctzll(hit) : idx;
     }
-    const int idx = (int)wave_umin(cand);
     if ((idx & (kWave - 1)) == lane) taken |= 1u << (idx / kWave);
-    const float p = expf(key_float(M) - m) / z;
-    psum += p;
     if (lane == k) {
-      my_p = p;
+      my_key = M;
       my_id = idx;
     }
   }
+  const float p = lane < K ? expf(key_float(my_key) - m) / z : 0.f;
+  float psum = 0.f;
+  for (int k = 0; k < K; ++k) psum += __shfl(p, k, kWave);  // slot order, every lane alike
   if (lane < K) {
-    ids_out[(size_t)t * K + lane] = my_id;
-    w_out[(size_t)t * K + lane] = renormalize ? my_p / psum : my_p;
+    const int q = t * K + lane;
+    const float w = renormalize ? p / psum : p;
+    ids_out[q] = my_id;
+    w_out[q] = w;
+    if (lds_ids) {
+      lds_ids[q] = my_id;
+      lds_w[q] = w;
+    }
   }
 }
 
@@ -132,51 +141,81 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   uint32_t flags = 0;
   if (t < a.T)
-    route_token(a.logits, t, a.E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags);
+    route_token(a.logits, t, a.E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
+                nullptr, nullptr);
   if (flags && (threadIdx.x & 63) == 0) atomicOr(&a.status[1], flags);
 }
 
-template <typename IdT>
+// Routes held in LDS by the planner (covers T = 1024 at top-8).
+constexpr int kLdsRoutes = 8192;
+static_assert(16 * 32 <= kLdsRoutes, "fused router (T <= 16, K <= 32) must fit the LDS routes");
+
+// LDS of the planner, carved by hand so the route arrays exist only when the
+// routes fit (R <= kLdsRoutes).
+struct PlanShared {
+  int wcnt[kPlanWaves][kMaxExperts];
+  int run[kMaxExperts];
+  int off[kMaxExperts];
+  int toff[kMaxExperts + 1];
+  uint32_t status;
+};
+
+template <typename IdT, bool LDSR>
 __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
-  __shared__ int s_wcnt[kPlanWaves][kMaxExperts];
-  __shared__ int s_run[kMaxExperts];
-  __shared__ int s_off[kMaxExperts];
-  __shared__ int s_toff[kMaxExperts + 1];
-  __shared__ uint32_t s_status;
+  __shared__ PlanShared sh;
+  // LDSR: ids, weights (fused router only) and ranks stay on chip.
+  __shared__ int s_ids[LDSR ? kLdsRoutes : 1];
+  __shared__ int s_rank[LDSR ? kLdsRoutes : 1];
+  __shared__ float s_w[LDSR ? kLdsRoutes : 1];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & (kWave - 1);
   const int E = a.E;
-  if (tid == 0) s_status = 0;
-  for (int e = tid; e < E; e += kPlanThreads) s_run[e] = 0;
+  if (tid == 0) sh.status = 0;
+  for (int e = tid; e < E; e += kPlanThreads) sh.run[e] = 0;
   uint32_t flags = 0;
 
+  bool ids_in_lds = false;
   if (a.route_logits) {
-    if (a.fuse_router) {
+    if (LDSR && a.fuse_router) {  // the host fuses only T <= 16: one token per wave
       for (int t = wave; t < a.T; t += kPlanWaves)
-        route_token(a.logits, t, E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags);
+        route_token(a.logits, t, E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
+                    s_ids, s_w);
+      ids_in_lds = true;
     } else if (tid == 0) {
       flags |= a.status[1];  // written by router_kernel earlier on this stream
       a.status[1] = 0;
     }
   }
-  // The router's global writes become visible to the whole workgroup here.
-  __threadfence_block();
-  __syncthreads();
+  // The router's results become visible to the whole workgroup here (they
+  // are read back from LDS when the routes fit there; otherwise from global
+  // memory, which needs the stronger fence).
+  if (LDSR && a.route_logits && a.fuse_router) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  } else {
+    __threadfence_block();
+    __syncthreads();
+  }
 
   const IdT *ids = (const IdT *)a.ids;
+  auto id_of = [&](int q) -> long long {
+    if (LDSR && ids_in_lds) return s_ids[q];
+    return (long long)ids[q];
+  };
   // Pass 1: canonical ranks, 1024 routes per round.
   for (int base = 0; base < a.R; base += kPlanThreads) {
-    for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) (&s_wcnt[0][0])[i] = 0;
+    for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) (&sh.wcnt[0][0])[i] = 0;
     __syncthreads();
     const int q = base + tid;
     const bool valid = q < a.R;
     long long idv = -1;
     float wv = 0.f;
     if (valid) {
-      idv = (long long)ids[q];
-      wv = a.weights[q];
+      idv = id_of(q);
+      wv = (LDSR && ids_in_lds) ? s_w[q] : a.weights[q];
     }
     const bool ok = valid && idv >= 0 && idv < E;
     if (valid && !ok) flags |= 1u;
@@ -190,20 +229,25 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
       match &= set ? b : ~b;
     }
     const int lrank = __popcll(match & lanemask_lt());
-    if (ok && lrank == 0) s_wcnt[wave][id] = __popcll(match);
+    if (ok && lrank == 0) sh.wcnt[wave][id] = __popcll(match);
     __syncthreads();
+    int rank = -1;
     if (ok) {
-      int r = s_run[id] + lrank;
-      for (int w = 0; w < wave; ++w) r += s_wcnt[w][id];
-      a.ranks[q] = r;
-    } else if (valid) {
-      a.ranks[q] = -1;
+      rank = sh.run[id] + lrank;
+      for (int w = 0; w < wave; ++w) rank += sh.wcnt[w][id];
+    }
+    if (valid) {
+      a.ranks[q] = rank;
+      if (LDSR) {
+        s_rank[q] = rank;
+        if (!ids_in_lds) s_ids[q] = ok ? id : -1;
+      }
     }
     __syncthreads();
     for (int e = tid; e < E; e += kPlanThreads) {
       int c = 0;
-      for (int w = 0; w < kPlanWaves; ++w) c += s_wcnt[w][e];
-      s_run[e] += c;
+      for (int w = 0; w < kPlanWaves; ++w) c += sh.wcnt[w][e];
+      sh.run[e] += c;
     }
     __syncthreads();
   }
@@ -216,7 +260,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = lane * 4 + j;
-      c[j] = e < E ? s_run[e] : 0;
+      c[j] = e < E ? sh.run[e] : 0;
       nt[j] = (c[j] + tb - 1) / tb;
       csum += c[j];
       tsum += nt[j];
@@ -236,25 +280,33 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
     for (int j = 0; j < 4; ++j) {
       const int e = lane * 4 + j;
       if (e < E) {
-        s_off[e] = crun;
-        s_toff[e] = trun;
+        sh.off[e] = crun;
+        sh.toff[e] = trun;
         a.counts[e] = c[j];
         a.offsets[e] = crun;
       }
       crun += c[j];
       trun += nt[j];
     }
-    if (lane == kWave - 1) s_toff[E] = trun;
+    if (lane == kWave - 1) sh.toff[E] = trun;
   }
   __syncthreads();
 
-  // Pass 3: map / inverse map (each thread rereads the ranks it wrote).
+  // Pass 3: map / inverse map.
   int valid_rows = 0;
-  if (E > 0) valid_rows = s_off[E - 1] + s_run[E - 1];
+  if (E > 0) valid_rows = sh.off[E - 1] + sh.run[E - 1];
   for (int q = tid; q < a.R; q += kPlanThreads) {
-    const long long idv = (long long)ids[q];
+    long long idv;
+    int rank;
+    if (LDSR) {
+      idv = s_ids[q];
+      rank = s_rank[q];
+    } else {
+      idv = (long long)ids[q];
+      rank = a.ranks[q];  // written by this thread in pass 1
+    }
     if (idv >= 0 && idv < E) {
-      const int p = s_off[idv] + a.ranks[q];
+      const int p = sh.off[idv] + rank;
       a.map[q] = p;
       a.row_route[p] = q;
       a.row_token[p] = q / a.K;
@@ -269,17 +321,17 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
 
   // Pass 4: task list, expert-major.
   for (int e = tid; e < E; e += kPlanThreads) {
-    const int c = s_run[e];
+    const int c = sh.run[e];
     const int tb = a.token_block;
-    int t0 = s_toff[e];
+    int t0 = sh.toff[e];
     for (int r0 = 0; r0 < c; r0 += tb, ++t0)
-      a.tasks[t0] = make_int4(e, s_off[e] + r0, min(tb, c - r0), 0);
+      a.tasks[t0] = make_int4(e, sh.off[e] + r0, min(tb, c - r0), 0);
   }
-  if (flags) atomicOr(&s_status, flags);
+  if (flags) atomicOr(&sh.status, flags);
   __syncthreads();
   if (tid == 0) {
-    *a.num_tasks = s_toff[E];
-    a.status[0] = s_status;
+    *a.num_tasks = sh.toff[E];
+    a.status[0] = sh.status;
     a.counters[0] = 0;
     a.counters[1] = 0;
   }
@@ -294,10 +346,14 @@ hipError_t launch_router(const RouteArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_route_plan(const RouteArgs &a, hipStream_t s) {
-  if (a.id64)
-    hipLaunchKernelGGL(route_plan_kernel<long long>, dim3(1), dim3(kPlanThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(route_plan_kernel<int32_t>, dim3(1), dim3(kPlanThreads), 0, s, a);
+  const bool lds = a.R <= kLdsRoutes;
+#define MOE_PLAN(T, L) hipLaunchKernelGGL((route_plan_kernel<T, L>), dim3(1), dim3(kPlanThreads), 0, s, a)
+  if (a.id64) {
+    if (lds) MOE_PLAN(long long, true); else MOE_PLAN(long long, false);
+  } else {
+    if (lds) MOE_PLAN(int32_t, true); else MOE_PLAN(int32_t, false);
+  }
+#undef MOE_PLAN
   return hipGetLastError();
 }
 

@@ -139,25 +139,31 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   u32x4 aq[S][NRB][AW];
   uint32_t sq[S][NRB][AW];
   Meta mq[S];
+  // m.unit < 0 marks a ring slot past the end: it loads one shared, cached
+  // row (expert 0, column block 0, lane row 0) instead of a whole unit.
   auto load_a = [&](const Meta &m, u32x4 (&buf)[NRB][AW], uint32_t (&sc)[NRB][AW]) {
+    const bool live = m.unit >= 0;
+    const int lr = live ? r : 0;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       if constexpr (W4) {
         const int G4 = H >> 7;
-        const size_t rbi = (size_t)m.expert * (2 * I / 16) + m.cb + (rb ? I / 16 : 0);
+        const size_t rbi = live ? (size_t)m.expert * (2 * I / 16) + m.cb + (rb ? I / 16 : 0) : 0;
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
           const size_t unit = rbi * G4 + (s0 >> 2) + i;
-          buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + lane];
-          sc[rb][i] = a.w4_scales[unit * 16 + r];
+          buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + (live ? lane : 0)];
+          sc[rb][i] = a.w4_scales[unit * 16 + lr];
         }
       } else {
         const uint16_t *row;
-        if (KIND == 0)
+        if (!live)
+          row = KIND == 0 ? a.gate_up : a.down;
+        else if (KIND == 0)
           row = a.gate_up + ((size_t)m.expert * 2 * I + (rb ? I : 0) + m.cb * 16 + r) * H;
         else
           row = a.down + ((size_t)m.expert * H + m.cb * 32 + rb * 16 + r) * I;
-        row += s0 * 32 + g * 8;
+        row += s0 * 32 + (live ? g * 8 : 0);
 #pragma unroll
         for (int i = 0; i < AW; ++i) buf[rb][i] = *(const u32x4 *)(row + i * 32);
       }
@@ -169,6 +175,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   for (int p = 0; p < S; ++p) {
     const int up = u_begin + p * G;
     mq[p] = meta_of(up < total ? up : u_begin);
+    if (up >= total) mq[p].unit = -1;
     load_a(mq[p], aq[p], sq[p]);
   }
   load_b(mq[0]);
@@ -253,10 +260,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
       }
     }
 
-    // Refill this slot with the unit S positions ahead (clamped: a cached
-    // re-read of the current unit near the end).
+    // Refill this slot with the unit S positions ahead.
     const int uf = u + S * G;
     mq[SL] = meta_of(uf < total ? uf : u);
+    if (uf >= total) mq[SL].unit = -1;
     load_a(mq[SL], aq[SL], sq[SL]);
     u += G;
     return u < total;
