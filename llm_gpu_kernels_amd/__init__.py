@@ -8,11 +8,13 @@ prepare/quantise call does, and raises if it has not been built.
 from .moe import (FrozenMoEPolicy, GemmConfig, PreparedMoE, PreparedRoutedMoE, prepare_configured_moe,
                   prepare_cuda_moe, prepare_moe, prepare_ranked_moe_launcher, prepare_routed_moe,
                   prepare_w4_layout_moe, prepare_w4_moe)
+from .attention import PreparedSegmentedGQA, prepare_cuda_gqa_compact, prepare_segmented_gqa
 from .weight_quant import PackedGateUp, TiledGateUp, dequantize_tiled, quantize_gate_up, tile_gate_up
 
 __all__ = [
     "FrozenMoEPolicy", "GemmConfig", "PreparedMoE", "PreparedRoutedMoE", "prepare_configured_moe",
     "prepare_cuda_moe", "prepare_moe", "prepare_ranked_moe_launcher", "prepare_routed_moe",
     "prepare_w4_layout_moe", "prepare_w4_moe", "PackedGateUp", "TiledGateUp", "dequantize_tiled",
-    "quantize_gate_up", "tile_gate_up",
+    "quantize_gate_up", "tile_gate_up", "PreparedSegmentedGQA", "prepare_segmented_gqa",
+    "prepare_cuda_gqa_compact",
 ]

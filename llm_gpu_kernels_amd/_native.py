@@ -34,6 +34,19 @@ class MoeLayout(ctypes.Structure):
                 ("fast_path", c_int32)]
 
 
+GQA_MAX_SEGMENTS = 4
+
+
+class GqaDesc(ctypes.Structure):
+    _fields_ = [("T", c_int32), ("Hq", c_int32), ("Hkv", c_int32), ("D", c_int32),
+                ("num_segments", c_int32), ("len", c_int32 * GQA_MAX_SEGMENTS),
+                ("q", c_void_p), ("out", c_void_p),
+                ("k", c_void_p * GQA_MAX_SEGMENTS), ("v", c_void_p * GQA_MAX_SEGMENTS),
+                ("k_stride", ctypes.c_int64 * GQA_MAX_SEGMENTS),
+                ("v_stride", ctypes.c_int64 * GQA_MAX_SEGMENTS),
+                ("scale", ctypes.c_float), ("workspace", c_void_p), ("workspace_bytes", c_size_t)]
+
+
 # name -> (restype, argtypes); the complete exported ABI of include/*.h.
 SIGNATURES = {
     "moe_abi_version": (c_int32, []),
@@ -51,6 +64,10 @@ SIGNATURES = {
     "moe_w4_tile": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "moe_w4_dequantize": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                     c_void_p]),
+    "gqa_seg_workspace_bytes": (c_int32, [POINTER(GqaDesc), POINTER(c_size_t)]),
+    "gqa_seg_plan_create": (c_int32, [POINTER(c_void_p), POINTER(GqaDesc)]),
+    "gqa_seg_plan_run": (c_int32, [c_void_p, c_void_p]),
+    "gqa_seg_plan_destroy": (None, [c_void_p]),
 }
 
 _LIB = None

@@ -1,0 +1,29 @@
+// Internal launch interface of the segmented-KV GQA attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kGqaMaxSegments = 4;
+
+struct GqaArgs {
+  const uint16_t *q;                     // [T, Hq, 128] bf16
+  uint16_t *out;                         // [T, Hq, 128] bf16
+  const uint16_t *k[kGqaMaxSegments];    // [len, Hkv, 128] bf16, token stride k_stride
+  const uint16_t *v[kGqaMaxSegments];
+  int64_t k_stride[kGqaMaxSegments];     // elements between consecutive tokens
+  int64_t v_stride[kGqaMaxSegments];
+  int len[kGqaMaxSegments];
+  int num_segments;                      // the last one is the current (causal) chunk
+  int T, Hq, Hkv, history;
+  float scale;
+  float *partial;                        // split-K partial states (nsplit > 1)
+};
+
+int gqa_num_splits(int T, int Hkv, int num_cus);
+size_t gqa_partial_bytes(int T, int Hq, int nsplit);
+hipError_t launch_gqa(const GqaArgs &a, int nsplit, hipStream_t s);
+
+}  // namespace moe

@@ -132,6 +132,16 @@ moe_layout compute_layout(const moe_desc *d) {
 
 }  // namespace
 
+namespace moe {
+int capi_fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+}  // namespace moe
+
 struct moe_plan {
   moe_desc d;
   moe_layout L;

@@ -37,6 +37,8 @@ def test_struct_sizes_match_header():
     # 10 int32 + 10 pointers + size_t; 13 size_t + 4 int32.
     assert ctypes.sizeof(N.MoeDesc) == 40 + 8 * 10 + 8
     assert ctypes.sizeof(N.MoeLayout) == 8 * 13 + 16
+    # 9 int32 (+pad) + 2 + 8 pointers + 8 int64 + float (+pad) + pointer + size_t.
+    assert ctypes.sizeof(N.GqaDesc) == 40 + 16 + 64 + 64 + 8 + 8 + 8
 
 
 def _desc(**kw):
