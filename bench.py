@@ -161,6 +161,44 @@ def measure(name, steps, warmup, device):
     return res, lay, plans
 
 
+def measure_attention(tokens, device, reps=20, per_graph=10):
+    """Segmented-KV GQA prefill: Q [T,32,128], KV segments
+    1024/512/256/T with 8 KV heads.  FLOPs = 32*4*128*(T*1792 + T(T+1)/2);
+    bytes = K,V once per KV head + Q + O.  One graph holds `per_graph` runs so
+    the figure is device time, not host graph-launch rate."""
+    from llm_gpu_kernels_amd import prepare_segmented_gqa
+    g = torch.Generator(device=device).manual_seed(tokens)
+    rnd = lambda shape: torch.randn(shape, generator=g, device=device).to(torch.bfloat16)
+    q = rnd((tokens, 32, 128))
+    segs = [(rnd((L, 8, 128)), rnd((L, 8, 128))) for L in (1024, 512, 256, tokens)]
+    plan = prepare_segmented_gqa(q, segs)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(per_graph):
+            plan.run()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    b.synchronize()
+    us = a.elapsed_time(b) / (reps * per_graph) * 1e3
+    flops = 32 * 4 * 128 * (tokens * 1792 + tokens * (tokens + 1) // 2)
+    nbytes = (1792 + tokens) * 8 * 128 * 2 * 2 + 2 * tokens * 32 * 128 * 2
+    tflops = flops / (us * 1e-6) / 1e12
+    gbs = nbytes / (us * 1e-6) / 1e9
+    attain = min(BF16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBS / 1e3)
+    return dict(workload=f"gqa-seg-t{tokens}", T=tokens, us=round(us, 2), tflops=round(tflops, 2),
+                hbm_gbs=round(gbs, 1), mfma_frac=round(tflops / BF16_PEAK_TFLOPS, 4),
+                attainable_roofline_frac=round(tflops / attain, 4),
+                arithmetic_intensity=round(flops / nbytes, 1))
+
+
 def cpu_baseline(lay, spec, budget_s=12.0):
     """FP32 CPU oracle (reference.py:17-45 restated) + CPU router, bounded sample."""
     from oracle.moe_oracle import moe_reference, route_topk
@@ -245,6 +283,11 @@ def main():
             sweep.append(r)
             del p
             torch.cuda.empty_cache()
+    attention = []
+    if not args.no_sweep:
+        for t in (32, 96, 256):
+            log(f"[bench] attention T={t}")
+            attention.append(measure_attention(t, device))
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")
@@ -268,6 +311,7 @@ def main():
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": main_res["layer_hbm_frac"]},
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "attention": attention,
     }
     print(json.dumps(line), flush=True)
 

@@ -9,7 +9,8 @@
  * negative MOE_E* code, message in moe_last_error().
  *
  * q [T, Hq, 128] bf16 contiguous; 1..4 KV segments, each k/v [L, Hkv, 128]
- * bf16 with inner strides (128, 1) and a token stride (elements) >= Hkv*128,
+ * bf16 with inner strides (128, 1) and a token stride (elements) >= Hkv*128
+ * and <= 2^25,
  * multiple of 8; the last segment is the current chunk (L == T, causal), the
  * others are fully visible history.  out [T, Hq, 128] bf16 contiguous.
  * Hq % Hkv == 0 and Hq / Hkv in {1, 2, 4, 8}; head_dim must be 128.
@@ -37,7 +38,7 @@ typedef struct gqa_seg_desc {
   const void *v[GQA_MAX_SEGMENTS];
   int64_t k_stride[GQA_MAX_SEGMENTS]; /* token stride in elements */
   int64_t v_stride[GQA_MAX_SEGMENTS];
-  float scale;                        /* 0 = 1/sqrt(D) */
+  float scale;                        /* <= 0 or non-finite: 1/sqrt(D) */
   void *workspace;                    /* split-K partials; >= gqa_seg_workspace_bytes() */
   size_t workspace_bytes;
 } gqa_seg_desc;

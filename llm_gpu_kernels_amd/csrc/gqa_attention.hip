@@ -9,19 +9,26 @@
 //   are fp32, probabilities are rounded to bf16 for the P.V product (as the
 //   reference does), the output is bf16.
 //
-// Design.  A workgroup owns one KV head, 16 query tokens and that head's
-// G = Hq/Hkv query heads (wave w = query head), so each K/V tile loaded into
-// LDS serves 16*G query rows.  Scores are computed transposed, S^T = K Q^T,
-// with 16x16x32 bf16 MFMAs: Q fragments stay in registers for the whole
-// kernel and the score tile lands in registers already in the A-operand
-// layout the P.V MFMA needs (lane l: token l%16, keys {4g..4g+3, 16+4g..})
-// so P never goes through LDS.  V is stored transposed in LDS (each lane
-// loads 4 keys x 2 dims as fully coalesced 256-byte rows and writes two
-// 8-byte columns), XOR-swizzled so the MFMA operand reads are conflict free.
-// K tiles use the same 16-byte XOR swizzle as the expert GEMMs.  When there
-// are too few (query block, KV head) pairs to fill the chip, the visible keys
-// are split across workgroups and a second kernel merges the partial
-// (max, sum, O) states in fixed split order.
+// Design.  A workgroup of four waves owns 64 query rows of one KV head: four
+// 16-row blocks, each one query head x 16 tokens (HPW heads x 64/HPW tokens).
+// The waves split the workgroup's visible keys into four contiguous ranges and
+// each wave runs its own online softmax over all 64 rows, 32 keys per step,
+// with no workgroup barrier in the loop:
+//   * scores are computed transposed, S^T = K Q^T, with 16x16x32 bf16 MFMAs;
+//     K fragments (A operand) are loaded from HBM straight into registers,
+//     Q fragments (B operand) stay in registers for the whole kernel, and the
+//     score tile lands in the A-operand layout of the P.V MFMA, so P never
+//     goes through LDS;
+//   * V rows are staged row-major (16-byte XOR swizzle) in a wave-private LDS
+//     area and read back with ds_read_b64_tr_b16, whose 16-lane transpose
+//     yields the B operand (8 keys x 1 dim per lane) directly;
+//   * the next step's K and V are prefetched into registers while the current
+//     step computes.
+// At the end the four waves' (max, sum, O) states are merged in LDS in fixed
+// wave order.  When there are too few workgroups to fill the chip the keys
+// are also split across workgroups and a second kernel merges the partial
+// states in fixed split order.
+#include <climits>
 #include "common.h"
 #include "gqa_internal.h"
 
@@ -30,250 +37,413 @@ namespace moe {
 namespace {
 
 constexpr int kD = 128;      // head_dim
-constexpr int kQB = 16;      // query tokens per workgroup
-constexpr int kKT = 64;      // keys per tile
+constexpr int kWaves = 4;    // waves per workgroup
+constexpr int kKC = 32;      // keys per wave step
+constexpr int kMaxSplits = 16;
+#ifndef GQA_ROW_BLOCKS
+#define GQA_ROW_BLOCKS 2
+#endif
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+#define GQA_LDS __attribute__((address_space(3)))
+
+__device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t sgpr64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
 }
 
-// Global key index -> pointer of key row (segment lookup; clamped keys are
-// the caller's business).
-__device__ __forceinline__ const uint16_t *key_row(const GqaArgs &a, const uint16_t *const *base,
-                                                   const int64_t *stride, int key, int kvh) {
-  int s = 0, off = key;
-#pragma unroll
-  for (int i = 0; i < kGqaMaxSegments - 1; ++i) {
-    if (s == i && i < a.num_segments - 1 && off >= a.len[i]) {
-      off -= a.len[i];
-      s = i + 1;
-    }
-  }
-  return base[s] + (int64_t)off * stride[s] + (int64_t)kvh * kD;
+// Loads through the global address space: generic (flat) loads also count in
+// the LDS wait counter, so every LDS wait of the compute loop would wait for
+// the next tile's prefetch as well.
+#define GQA_GLOBAL __attribute__((address_space(1)))
+template <class V>
+__device__ __forceinline__ V gload_as(const void *p) {
+  return *(const GQA_GLOBAL V *)(const GQA_GLOBAL void *)p;
 }
 
-// K tile byte offset of 16-byte chunk c of key row r ([64][128] bf16, 256-B rows).
+// Byte offset of 16-byte chunk c of row r in a row-major tile of 256-byte rows
+// (128 bf16), chunks XOR-swizzled by the row's low four bits.
 __device__ __forceinline__ int k_off(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
-// V^T tile byte offset of 8-byte chunk c (4 keys) of dim row d ([128][64] bf16).
-__device__ __forceinline__ int v_off(int d, int c) { return d * 128 + ((c ^ (d & 15)) << 3); }
 
-template <int G>
-__global__ __launch_bounds__(64 * G) void gqa_partial_kernel(GqaArgs a) {
-  constexpr int kThreads = 64 * G;
-  __shared__ __attribute__((aligned(16))) uint8_t s_k[kKT * kD * 2];
-  __shared__ __attribute__((aligned(16))) uint8_t s_v[kKT * kD * 2];
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a+b receives
+// element b of the 8-byte rows addressed by lanes a, a+4, a+8, a+12.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint8_t *lds, int byte_off) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GQA_LDS i16x4 *)(lds + byte_off));
+  return __builtin_bit_cast(u32x2, v);
+}
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+// Reductions over the four 16-lane rows holding one token's keys (lanes
+// l, l^16, l^32, l^48) with the gfx950 lane-swap instructions (VALU only):
+// swapping halves/rows of two copies leaves each lane with its own value and
+// its partner's, combined in the same order on both lanes.
+__device__ __forceinline__ float rows_max(float x) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// Running maxima lag the true maxima by at most this much (base-2 exponent),
+// so probabilities stay <= 2^8 and O is rescaled only when a row's maximum
+// grows past it (softmax is invariant to the reference maximum).
+constexpr float kRescaleSlack = 8.f;
+
+// One step's keys: up to 32 consecutive keys that all lie in one segment, so
+// the row addresses are (segment base) + row * (segment stride) with
+// wave-uniform base and stride.
+struct Tile {
+  int n;            // valid rows (1..32)
+  int local0;       // index of the first key within its segment
+  bool causal;      // the keys lie in the current (causal) segment
+  const uint8_t *kb, *vb;  // row 0 (KV head offset included)
+  uint32_t ksb, vsb;       // token strides in bytes (32 * stride < 2^31, checked on the host)
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.
+// The 1-D grid is remapped so that XCD x runs a contiguous range of logical
+// workgroups, ordered KV-head major: the workgroups that read the same K/V
+// rows then share one L2.  Returns the logical index of this workgroup.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_logical_block(int id, int n) {
+  const int x = id % kXcds, slot = id / kXcds, per = n / kXcds, extra = n % kXcds;
+  return x * per + min(x, extra) + slot;
+}
+
+// RB 16-row blocks per wave; HPW query heads per workgroup (HPW divides RB);
+// row block rb is (head rb % HPW, token block rb / HPW).  With RB = 2 the
+// kernel fits two workgroups per CU (two waves per SIMD).
+template <int RB, int HPW>
+__global__ __launch_bounds__(64 * kWaves, 4 / RB) void gqa_fwd_kernel(GqaArgs a, int head_groups,
+                                                                      int nqb, int nsplit) {
+  constexpr int kRB = RB;
+  constexpr int QT = 16 * (kRB / HPW);                 // tokens per workgroup
+  constexpr int kStage = kKC * kD * 2;                 // V staging per wave (8 KB)
+  constexpr int kOBytes = kWaves * kRB * 8 * 64 * 16;  // merge: O states (32 KB per row block)
+  constexpr int kMLBytes = kWaves * kRB * 16 * 2 * 4;  // merge: (m, l) per row
+  static_assert(kWaves * kStage <= kOBytes, "V staging aliases the merge area");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kOBytes + kMLBytes];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = sgpr(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int q0 = blockIdx.x * kQB;
-  const int kvh = blockIdx.y;
-  const int split = blockIdx.z, nsplit = gridDim.z;
-  const int head = kvh * G + wave;
+  // Logical workgroup = ((KV head group) * nsplit + split) * nqb + query block.
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int qb = lb % nqb, split = (lb / nqb) % nsplit, kvg = lb / (nqb * nsplit);
+  const int q0 = qb * QT;
+  const int G = a.Hq / a.Hkv;
+  const int kvh = kvg / head_groups;
+  const int h0 = kvh * G + (kvg % head_groups) * HPW;
   const int T = a.T;
   const int hist = a.history;
 
-  // Visible keys of this query block: all history + current keys < q0 + 16.
-  const int cur_vis = min(T, q0 + kQB);
-  const int nvis = hist + cur_vis;
-  const int k_beg = (int)((long long)nvis * split / nsplit);
-  const int k_end = (int)((long long)nvis * (split + 1) / nsplit);
+  // Segment starts (global key index); absent segments start at INT_MAX and
+  // empty ones coincide with the next start, so the count below skips them.
+  const int nseg = sgpr(a.num_segments);
+  const int l0 = sgpr(a.len[0]), l1 = sgpr(a.len[1]), l2 = sgpr(a.len[2]);
+  const int st1 = nseg > 1 ? l0 : INT_MAX;
+  const int st2 = nseg > 2 ? l0 + l1 : INT_MAX;
+  const int st3 = nseg > 3 ? l0 + l1 + l2 : INT_MAX;
 
-  // Q fragments (B operand of S^T = K Q^T): lane l -> token q0 + l%16,
-  // dims 32*ks + 8*(l/16) .. +8.
-  u32x4 qf[4];
-  {
-    const int tok = q0 + r < T ? q0 + r : T - 1;
-    const uint16_t *qp = a.q + ((int64_t)tok * a.Hq + head) * kD + 8 * g;
+  // Visible keys of the workgroup: all history + current keys < q0 + QT, in
+  // 32-key chunks split across workgroups (split) and then across waves.
+  const int nvis = hist + min(T, q0 + QT);
+  const int nch = (nvis + kKC - 1) / kKC;
+  const int c0 = (int)((long long)nch * split / nsplit), c1 = (int)((long long)nch * (split + 1) / nsplit);
+  const int cw0 = c0 + (c1 - c0) * wave / kWaves, cw1 = c0 + (c1 - c0) * (wave + 1) / kWaves;
+  const int k_beg = cw0 * kKC, k_end = min(cw1 * kKC, nvis);
+
+  auto tile_at = [&](int pos) __attribute__((always_inline)) {
+    Tile t;
+    const int seg = sgpr((pos >= st1) + (pos >= st2) + (pos >= st3));
+    const int sbeg = seg == 0 ? 0 : seg == 1 ? st1 : seg == 2 ? st2 : st3;
+    const int send = seg == 0 ? st1 : seg == 1 ? st2 : seg == 2 ? st3 : INT_MAX;
+    t.n = min(kKC, min(send, k_end) - pos);
+    t.local0 = pos - sbeg;
+    t.causal = seg == nseg - 1;
+    // seg is wave-uniform, so these are scalar loads of the kernel arguments.
+    const int64_t ks = a.k_stride[seg], vs = a.v_stride[seg];
+    t.ksb = (uint32_t)(2 * ks);
+    t.vsb = (uint32_t)(2 * vs);
+    t.kb = (const uint8_t *)(a.k[seg] + (int64_t)t.local0 * ks + (int64_t)kvh * kD);
+    t.vb = (const uint8_t *)(a.v[seg] + (int64_t)t.local0 * vs + (int64_t)kvh * kD);
+    return t;
+  };
+
+  // Q fragments (B operand of S^T = K Q^T): lane l -> token l%16 of the row
+  // block, dims 32*ks + 8*(l/16) .. +8.
+  u32x4 qf[kRB][4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = *(const u32x4 *)(qp + 32 * ks);
+  for (int rb = 0; rb < kRB; ++rb) {
+    int tok = q0 + 16 * (rb / HPW) + r;
+    tok = tok < T ? tok : T - 1;
+    const uint16_t *qp = a.q + ((int64_t)tok * a.Hq + h0 + rb % HPW) * kD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[rb][ks] = gload_as<u32x4>(qp + 32 * ks);
   }
 
-  // Online softmax state for the lane's token (l % 16), fp32, base-2 domain.
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4 o[8];
+  // Online softmax state of the lane's token (l % 16) per row block, fp32,
+  // base-2 domain; O[rb][dt] holds tokens 4*(l/16) + i, dims 16*dt + l%16.
+  float m_run[kRB], l_run[kRB];
+  f32x4 o[kRB][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < kRB; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[rb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const float sl2 = a.scale * kLog2e;
 
-  // Register staging of the next tile: K 64 rows x 256 B = 16 KB -> 16 B x
-  // (1024 / kThreads * ... ) per thread; V as 4-key x 2-dim dword columns.
-  constexpr int K_LOADS = kKT * kD * 2 / 16 / kThreads;  // 16-B loads per thread
-  constexpr int V_QUADS = kKT / 4 / G;                    // 4-key groups per wave
-  u32x4 kr[K_LOADS];
-  uint32_t vr[V_QUADS][4];
-  const uint16_t *kbase[kGqaMaxSegments] = {a.k[0], a.k[1], a.k[2], a.k[3]};
-  const uint16_t *vbase[kGqaMaxSegments] = {a.v[0], a.v[1], a.v[2], a.v[3]};
-
-  auto gload = [&](int t0) {
+  // Register prefetch.  K: A-operand fragments, lane l -> key 16*kt + l%16,
+  // dims 32*ks + 8*(l/16).  V: whole 256-byte rows, 16 lanes per row.  Rows
+  // past the step's end re-read row 0 (masked out below).  The next step's V
+  // is requested as soon as this step's V is in LDS, the next step's K as soon
+  // as this step's score MFMAs have read their K fragments, so one register
+  // set of each suffices.
+  u32x4 kf[2][4], vn[8];
+  // Addresses are a scalar row base plus one per-lane offset per tile, with
+  // the column offset in the instruction's immediate field; only a partial
+  // tile (rows past its end clamp to its last row) needs per-row lane math.
+  auto load_k = [&](const Tile &t) __attribute__((always_inline)) {
+    if (t.n == kKC) {
+      const uint32_t lo = r * t.ksb + 16 * g;
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = i * kThreads + tid;  // 16-B chunk index within the tile
-      const int row = idx >> 4, c = idx & 15;
-      int key = t0 + row;
-      key = key < k_end ? key : k_beg;  // clamp: masked below, any valid row will do
-      kr[i] = *(const u32x4 *)(key_row(a, kbase, a.k_stride, key, kvh) + 8 * c);
-    }
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int qd = 0; qd < V_QUADS; ++qd) {
-      const int kq = (wave * V_QUADS + qd) * 4;
+        for (int ks = 0; ks < 4; ++ks) kf[kt][ks] = gload_as<u32x4>(t.kb + 16 * kt * t.ksb + lo + 64 * ks);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int key = t0 + kq + j;
-        key = key < k_end ? key : k_beg;
-        vr[qd][j] = *(const uint32_t *)(key_row(a, vbase, a.v_stride, key, kvh) + 2 * lane);
+      for (int kt = 0; kt < 2; ++kt) {
+        const uint32_t off = min(16 * kt + r, t.n - 1) * t.ksb + 16 * g;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kf[kt][ks] = gload_as<u32x4>(t.kb + off + 64 * ks);
       }
     }
   };
-  auto sts = [&]() {
+  auto load_v = [&](const Tile &t) __attribute__((always_inline)) {
+    if (t.n == kKC) {
+      const uint32_t lo = g * t.vsb + 16 * r;
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = i * kThreads + tid;
-      *(u32x4 *)(s_k + k_off(idx >> 4, idx & 15)) = kr[i];
-    }
+      for (int i = 0; i < 8; ++i) vn[i] = gload_as<u32x4>(t.vb + 4 * i * t.vsb + lo);
+    } else {
 #pragma unroll
-    for (int qd = 0; qd < V_QUADS; ++qd) {
-      const int c = wave * V_QUADS + qd;  // 4-key chunk index
-      u32x2 lo, hi;  // dims 2*lane and 2*lane+1 of keys 4c..4c+3
-      lo[0] = (vr[qd][0] & 0xffffu) | (vr[qd][1] << 16);
-      lo[1] = (vr[qd][2] & 0xffffu) | (vr[qd][3] << 16);
-      hi[0] = (vr[qd][0] >> 16) | (vr[qd][1] & 0xffff0000u);
-      hi[1] = (vr[qd][2] >> 16) | (vr[qd][3] & 0xffff0000u);
-      *(u32x2 *)(s_v + v_off(2 * lane, c)) = lo;
-      *(u32x2 *)(s_v + v_off(2 * lane + 1, c)) = hi;
+      for (int i = 0; i < 8; ++i)
+        vn[i] = gload_as<u32x4>(t.vb + (min(4 * i + g, t.n - 1) * t.vsb + 16 * r));
     }
   };
 
-  if (k_beg < k_end) gload(k_beg);
-  for (int t0 = k_beg; t0 < k_end; t0 += kKT) {
-    sts();
-    lds_barrier();
-    if (t0 + kKT < k_end) gload(t0 + kKT);
+  uint8_t *stage = smem + wave * kStage;
+  // B operand of P.V from the staged V rows: lane l (group g = l/16,
+  // a = l%4, j = (l%16)/4) addresses row 16h + 4g + j, dims 16dt + 4a .. +3;
+  // after the transpose lane l holds dim 16dt + l%16 of keys 16h + 4g + 0..3.
+  const int tr_row = 4 * g + (r >> 2), tr_a = r & 3;
 
-    // S^T tile: 4 subtiles of 16 keys; lane holds keys 16*kt + 4g + i, token r.
-    f32x4 s[4];
+  int pos = k_beg;
+  Tile cur = tile_at(pos);
+  if (pos < k_end) {
+    load_k(cur);
+    load_v(cur);
+  }
+  while (pos < k_end) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 kf = *(const u32x4 *)(s_k + k_off(16 * kt + r, 4 * ks + g));
-        s[kt] = mfma16(kf, qf[ks], s[kt]);
-      }
-    }
-    // Mask, scale, tile max.
-    const int tok = q0 + r;
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = t0 + 16 * kt + 4 * g + i;
-        const bool ok = key < k_end && tok < T && (key < hist || key - hist <= tok);
-        s[kt][i] = ok ? s[kt][i] * sl2 : -INFINITY;
-        tmax = fmaxf(tmax, s[kt][i]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
-    float psum = 0.f;
-    u32x4 pa[2];  // A operand of P.V for key steps kk = 0, 1
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = s[kt][i] == -INFINITY ? 0.f : exp2f(s[kt][i] - m_new);
-        psum += p[i];
-      }
-      pa[kt >> 1][(kt & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
-      pa[kt >> 1][(kt & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+    for (int i = 0; i < 8; ++i) *(u32x4 *)(stage + k_off(4 * i + g, r)) = vn[i];
+    const int next = pos + cur.n;
+    const Tile nxt = tile_at(next);
+    const bool more = next < k_end;
+    if (more) load_v(nxt);
 
-    // Rescale O: lane holds tokens 4g + i; their alpha lives in lanes 4g + i.
-    float al[4];
+    // S^T: lane holds keys 16*kt + 4g + i of token r, per row block.
+    f32x4 s[kRB][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, 64);
+    for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+      for (int kt = 0; kt < 2; ++kt) s[rb][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[dt][i] *= al[i];
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[rb][kt] = mfma16(kf[kt][ks], qf[rb][ks], s[rb][kt]);
+    if (more) load_k(nxt);
 
-    // O += P V over the tile's 64 keys (two 32-key steps).
+    u32x4 vb[8];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = 16 * dt + r;
-        u32x4 vb;
-        const u32x2 v0 = *(const u32x2 *)(s_v + v_off(d, 8 * kk + g));
-        const u32x2 v1 = *(const u32x2 *)(s_v + v_off(d, 8 * kk + 4 + g));
-        vb[0] = v0[0];
-        vb[1] = v0[1];
-        vb[2] = v1[0];
-        vb[3] = v1[1];
-        o[dt] = mfma16(pa[kk], vb, o[dt]);
-      }
+    for (int dt = 0; dt < 8; ++dt) {
+      const int c = 2 * dt + (tr_a >> 1), w = 8 * (tr_a & 1);
+      const u32x2 lo = lds_read_tr16(stage, k_off(tr_row, c) + w);
+      const u32x2 hi = lds_read_tr16(stage, k_off(16 + tr_row, c) + w);
+      vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
-    lds_barrier();
+
+    const bool full = cur.n == kKC && !cur.causal;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      // Mask (raw scores): rows past the step's end and, in the current
+      // segment, keys after the token (key j of the current chunk is token j).
+      if (!full) {
+        const int tok = q0 + 16 * (rb / HPW) + r;
+        const int lim = cur.causal ? min(cur.n - 1, tok - cur.local0) : cur.n - 1;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[rb][kt][i] = 16 * kt + 4 * g + i <= lim ? s[rb][kt][i] : -INFINITY;
+      }
+      // The scale is positive, so the maximum is taken on raw scores and the
+      // scale is folded into the exponent's FMA (base-2 domain).
+      float tmax = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
+                         fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3])));
+      tmax = rows_max(tmax) * sl2;
+      // Rescale only when some row's maximum outgrows the slack (wave-uniform
+      // branch).  A row with no visible key so far keeps m = -inf.
+      if (__builtin_amdgcn_ballot_w64(tmax > m_run[rb] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[rb], tmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[rb] - (m_new == -INFINITY ? 0.f : m_new));
+        l_run[rb] *= alpha;
+        m_run[rb] = m_new;
+        float al[4];  // O rows are tokens 4g + i; their alpha lives in lanes 4g + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[rb][dt][i] *= al[i];
+      }
+      const float neg_m = m_run[rb] == -INFINITY ? 0.f : -m_run[rb];
+      float psum = 0.f;
+      float p[2][4];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][kt][i], sl2, neg_m));
+          psum += p[kt][i];
+        }
+      // A operand of P.V: slots 0..3 = keys 4g + i, slots 4..7 = keys 16 + 4g + i.
+      const u32x4 pa = u32x4{pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                             pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+      l_run[rb] += rows_sum(psum);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[rb][dt] = mfma16(pa, vb[dt], o[rb][dt]);
+    }
+    pos = next;
+    cur = nxt;
   }
 
-  // Epilogue.  Lane holds O[tokens 4g + i][dims 16*dt + r]; the row sums and
-  // maxima of those tokens live in lanes 4g + i.
-  float lt[4], mt[4];
+  // Merge of the four waves' states, fixed wave order.  The staging areas
+  // are reused, so every wave must be past its loop first.
+  float *ost = (float *)smem;               // [wave][rb][dt][lane] x 4
+  float *ml = (float *)(smem + kOBytes);    // [wave][rb][row] x {m, l}
+  __syncthreads();
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *(f32x4 *)(ost + (((wave * kRB + rb) * 8 + dt) * 64 + lane) * 4) = o[rb][dt];
+    if (g == 0) *(f32x2_t *)(ml + ((wave * kRB + rb) * 16 + r) * 2) = f32x2_t{m_run[rb], l_run[rb]};
+  }
+  __syncthreads();
+
+  // Wave w finalises row block w % RB, dims 64 * (w / RB) .. +64 when RB = 2
+  // (all 128 dims when RB = 4): lane holds tokens 4g + i, dims 16dt + r.
+  static_assert(kWaves % kRB == 0, "row blocks are shared out evenly over the waves");
+  constexpr int kDT = 8 * kRB / kWaves;  // 16-dim column tiles per finalising wave
+  const int rb = wave % kRB, dt0 = (wave / kRB) * kDT;
+  const int head = h0 + rb % HPW;
+  const int tb0 = q0 + 16 * (rb / HPW);
+  float wgt[kWaves][4], M[4], L[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    lt[i] = __shfl(l_run, 4 * g + i, 64);
-    mt[i] = __shfl(m_run, 4 * g + i, 64);
+    M[i] = -INFINITY;
+#pragma unroll
+    for (int src = 0; src < kWaves; ++src) M[i] = fmaxf(M[i], ml[((src * kRB + rb) * 16 + 4 * g + i) * 2]);
+    L[i] = 0.f;
+#pragma unroll
+    for (int src = 0; src < kWaves; ++src) {
+      const f32x2_t st = *(const f32x2_t *)(ml + ((src * kRB + rb) * 16 + 4 * g + i) * 2);
+      wgt[src][i] = st[0] == -INFINITY ? 0.f : exp2f(st[0] - M[i]);
+      L[i] += wgt[src][i] * st[1];
+    }
+  }
+  f32x4 acc[kDT];
+#pragma unroll
+  for (int j = 0; j < kDT; ++j) {
+    acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int src = 0; src < kWaves; ++src) {
+      const f32x4 v = *(const f32x4 *)(ost + (((src * kRB + rb) * 8 + dt0 + j) * 64 + lane) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][i] += wgt[src][i] * v[i];
+    }
   }
   if (nsplit == 1) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = q0 + 4 * g + i;
+      const int tok = tb0 + 4 * g + i;
       if (tok >= T) continue;
-      const float inv = lt[i] > 0.f ? 1.0f / lt[i] : 0.f;
-      uint16_t *op = a.out + ((int64_t)tok * a.Hq + head) * kD + r;
+      const float inv = L[i] > 0.f ? 1.0f / L[i] : 0.f;
+      uint16_t *op = a.out + ((int64_t)tok * a.Hq + head) * kD + 16 * dt0 + r;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) op[16 * dt] = (uint16_t)(pack_bf16x2(o[dt][i] * inv, 0.f) & 0xffffu);
+      for (int j = 0; j < kDT; ++j) op[16 * j] = (uint16_t)(pack_bf16x2(acc[j][i] * inv, 0.f) & 0xffffu);
     }
   } else {
     // Partial state: [split][token][head] {m, l, O[128]} fp32.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = q0 + 4 * g + i;
+      const int tok = tb0 + 4 * g + i;
       if (tok >= T) continue;
       float *pp = a.partial + (((int64_t)split * T + tok) * a.Hq + head) * (kD + 2);
-      if (r == 0) {
-        pp[0] = mt[i];
-        pp[1] = lt[i];
+      if (r == 0 && dt0 == 0) {
+        pp[0] = M[i];
+        pp[1] = L[i];
       }
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) pp[2 + 16 * dt + r] = o[dt][i];
+      for (int j = 0; j < kDT; ++j) pp[2 + 16 * (dt0 + j) + r] = acc[j][i];
     }
   }
 }
 
-// out[t][h] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, splits in order.
+// out[t][h] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s over the splits,
+// combined in fixed split order, four splits per round trip: the loads of a
+// group are issued together (a plain loop over a run-time count would issue
+// one round trip per split) and the running maximum is rescaled between groups.
 __global__ __launch_bounds__(128) void gqa_merge_kernel(GqaArgs a, int nsplit) {
+  constexpr int kGroup = 4;
   const int th = blockIdx.x;  // token * Hq + head
   const int d = threadIdx.x;  // 0..127
   const float *base = a.partial + (int64_t)th * (kD + 2);
   const int64_t sstride = (int64_t)a.T * a.Hq * (kD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[s * sstride]);
-  float num = 0.f, den = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float *p = base + s * sstride;
-    const float w = p[0] == -INFINITY ? 0.f : exp2f(p[0] - M);
-    den += w * p[1];
-    num += w * p[2 + d];
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kGroup) {
+    float m[kGroup], l[kGroup], ov[kGroup];
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      const float *p = base + min(s0 + j, nsplit - 1) * sstride;
+      m[j] = gload_as<float>(p);
+      l[j] = gload_as<float>(p + 1);
+      ov[j] = gload_as<float>(p + 2 + d);
+    }
+    float Mn = M;
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) Mn = s0 + j < nsplit ? fmaxf(Mn, m[j]) : Mn;
+    if (Mn == -INFINITY) continue;  // nothing visible so far
+    const float r = M == -INFINITY ? 0.f : exp2f(M - Mn);
+    num *= r;
+    den *= r;
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      const float w = (s0 + j >= nsplit || m[j] == -INFINITY) ? 0.f : exp2f(m[j] - Mn);
+      den += w * l[j];
+      num += w * ov[j];
+    }
+    M = Mn;
   }
   const float v = den > 0.f ? num / den : 0.f;
   a.out[(int64_t)th * kD + d] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
@@ -281,12 +451,19 @@ __global__ __launch_bounds__(128) void gqa_merge_kernel(GqaArgs a, int nsplit) {
 
 }  // namespace
 
-int gqa_num_splits(int T, int Hkv, int num_cus) {
-  const int blocks = ((T + kQB - 1) / kQB) * Hkv;
-  if (blocks <= 0) return 1;
-  int s = (2 * num_cus + blocks - 1) / blocks;  // aim for ~2 workgroups per CU
+// Row blocks per wave and query heads per workgroup of the launched variant.
+constexpr int kLaunchRB = GQA_ROW_BLOCKS;
+int gqa_heads_per_wg(int G) { return G < kLaunchRB ? G : kLaunchRB; }
+
+int gqa_num_splits(int T, int Hq, int Hkv, int num_cus) {
+  const int G = Hq / Hkv, hpw = gqa_heads_per_wg(G);
+  const int qt = 16 * (kLaunchRB / hpw);
+  const int wgs = ((T + qt - 1) / qt) * Hkv * (G / hpw);
+  if (wgs <= 0) return 1;
+  const int per_cu = 4 / kLaunchRB;  // resident workgroups per CU
+  int s = (num_cus * per_cu + wgs - 1) / wgs;
   if (s < 1) s = 1;
-  if (s > 16) s = 16;
+  if (s > kMaxSplits) s = kMaxSplits;
   return s;
 }
 
@@ -296,13 +473,16 @@ size_t gqa_partial_bytes(int T, int Hq, int nsplit) {
 
 hipError_t launch_gqa(const GqaArgs &a, int nsplit, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
-  const int G = a.Hq / a.Hkv;
-  const dim3 grid((a.T + kQB - 1) / kQB, a.Hkv, nsplit);
-  switch (G) {
-    case 1: hipLaunchKernelGGL(gqa_partial_kernel<1>, grid, dim3(64), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(gqa_partial_kernel<2>, grid, dim3(128), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(gqa_partial_kernel<4>, grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL(gqa_partial_kernel<8>, grid, dim3(512), 0, s, a); break;
+  const int G = a.Hq / a.Hkv, hpw = gqa_heads_per_wg(G);
+  const int qt = 16 * (kLaunchRB / hpw), groups = G / hpw;
+  const int nqb = (a.T + qt - 1) / qt;
+  const dim3 grid(nqb * a.Hkv * groups * nsplit), block(64 * kWaves);
+  switch (hpw) {
+    case 1: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 1>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+    case 2: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 2>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+#if GQA_ROW_BLOCKS == 4
+    case 4: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 4>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+#endif
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();

@@ -25,6 +25,8 @@ struct gqa_seg_plan {
 
 namespace {
 
+constexpr int64_t kMaxTokenStride = 1LL << 25;
+
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 int validate(const gqa_seg_desc *d, int num_cus, int *nsplit) {
@@ -51,12 +53,16 @@ int validate(const gqa_seg_desc *d, int num_cus, int *nsplit) {
         d->v_stride[s] % 8)
       return capi_fail(MOE_EINVAL, "segment %d token stride must be >= %lld and a multiple of 8",
                        s, (long long)minst);
+    // The kernel addresses 32 consecutive rows with 32-bit byte offsets.
+    if (d->k_stride[s] > kMaxTokenStride || d->v_stride[s] > kMaxTokenStride)
+      return capi_fail(MOE_EINVAL, "segment %d token stride must be <= %lld elements", s,
+                       (long long)kMaxTokenStride);
   }
   if (d->T > 0 && (!d->q || !d->out || !aligned16(d->q) || !aligned16(d->out)))
     return capi_fail(MOE_EINVAL, "q/out must be non-null and 16-byte aligned");
   if ((long long)d->T * d->Hq * 128 >= (1LL << 31))
     return capi_fail(MOE_EINVAL, "T * Hq * 128 must be < 2^31");
-  *nsplit = moe::gqa_num_splits(d->T, d->Hkv, num_cus);
+  *nsplit = moe::gqa_num_splits(d->T, d->Hq, d->Hkv, num_cus);
   return MOE_OK;
 }
 
@@ -111,7 +117,7 @@ int gqa_seg_plan_create(gqa_seg_plan **out, const gqa_seg_desc *d) {
   a.T = d->T;
   a.Hq = d->Hq;
   a.Hkv = d->Hkv;
-  a.scale = d->scale > 0.f ? d->scale : 1.0f / sqrtf((float)d->D);
+  a.scale = (d->scale > 0.f && d->scale < INFINITY) ? d->scale : 1.0f / sqrtf((float)d->D);
   a.partial = (float *)d->workspace;
   p->nsplit = ns;
   p->device = dev;

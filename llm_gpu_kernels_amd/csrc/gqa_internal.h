@@ -22,7 +22,7 @@ struct GqaArgs {
   float *partial;                        // split-K partial states (nsplit > 1)
 };
 
-int gqa_num_splits(int T, int Hkv, int num_cus);
+int gqa_num_splits(int T, int Hq, int Hkv, int num_cus);
 size_t gqa_partial_bytes(int T, int Hq, int nsplit);
 hipError_t launch_gqa(const GqaArgs &a, int nsplit, hipStream_t s);
 
