@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   extern __shared__ f32x4 s_red[];  // [2][kWaves][NRB][MT][64]
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int lane = tid & (kWave - 1);
   const int r = lane & 15, g = lane >> 4;
   const int H = a.H, I = a.I;
@@ -84,8 +84,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   const MOE_CONST int32_t *row_idx = as_const(KIND == 0 ? a.row_token : a.row_route);
 
   // Unit metadata: scalars, plus one VGPR whose lane k < ROWS holds the
-  // token (gate/up) or route (down) of the task's row k, built with
-  // lane selects from scalar loads and read back with a lane shuffle.
+  // token (gate/up) or route (down) of the task's row k (one vector load; the
+  // index arrays carry 32 ints of slack past the last row).
+  const int32_t *row_vec = KIND == 0 ? a.row_token : a.row_route;
   struct Meta {
     int unit, cb, expert, row0, rows;
     int idxv;
@@ -98,17 +99,14 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
     m.expert = tasks[4 * t];
     m.row0 = tasks[4 * t + 1];
     m.rows = tasks[4 * t + 2];
-    int v = 0;
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {  // in-bounds: the index arrays carry 32 ints of slack
-      const int sv = row_idx[m.row0 + k];
-      v = lane == k ? sv : v;
-    }
-    m.idxv = v;
+    m.idxv = row_vec[m.row0 + (lane & 31)];
     return m;
   };
 
-  // B operand: [MT][SPW] fragments of this wave's K-slice.
+  // B operand: [MT][SPW] fragments of this wave's K-slice.  Rows past the
+  // task's end load row 0 of x (gate/up) or of act (down) instead, finite
+  // data that is never zeroed: an MFMA output column depends only on its own
+  // B column and the epilogue never stores those columns.
   u32x4 bfr[MT][SPW];
   auto load_b = [&](const Meta &m) {
 #pragma unroll
@@ -122,50 +120,49 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
         row = (size_t)(ok ? m.row0 + j : 0) * I;
       const uint16_t *src = (KIND == 0 ? a.x : a.act) + row + s0 * 32 + g * 8;
 #pragma unroll
-      for (int i = 0; i < SPW; ++i) {
-        const u32x4 v = *(const u32x4 *)(src + i * 32);
-        bfr[mt][i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int i = 0; i < SPW; ++i) bfr[mt][i] = *(const u32x4 *)(src + i * 32);
     }
   };
 
   // A operand: bf16 -> [NRB][SPW] fragments; W4 -> [NRB][SPW/4] words + scales.
   // A ring of S unit slots keeps S-1 units of weights in flight (W4 units are
-  // 4x smaller, so they need a deeper ring).  Slots are compile-time indices
+  // 4x smaller, so they need a deeper ring; three slots keep the kernel within
+  // 128 VGPRs, i.e. two workgroups per CU).  Slots are compile-time indices
   // of an unrolled loop: copying a register whose load is still in flight
   // would make the wave wait for it.
   constexpr int AW = W4 ? SPW / 4 : SPW;
-  constexpr int S = W4 ? 4 : 2;
+  constexpr int S = W4 ? 3 : 2;
   u32x4 aq[S][NRB][AW];
   uint32_t sq[S][NRB][AW];
   Meta mq[S];
-  // m.unit < 0 marks a ring slot past the end: it loads one shared, cached
-  // row (expert 0, column block 0, lane row 0) instead of a whole unit.
+  // m.unit < 0 marks a ring slot past the end: it reads the first unit of the
+  // weights (expert 0, column block 0), which every such slot shares through
+  // the cache, with the normal lane offsets -- so every address is a scalar
+  // base plus a fixed per-lane offset and the loads need no vector math.
+  const uint32_t lane_a = KIND == 0 ? (uint32_t)(r * H + g * 8) * 2u : (uint32_t)(r * I + g * 8) * 2u;
   auto load_a = [&](const Meta &m, u32x4 (&buf)[NRB][AW], uint32_t (&sc)[NRB][AW]) {
     const bool live = m.unit >= 0;
-    const int lr = live ? r : 0;
+    const int ex = live ? m.expert : 0, cb = live ? m.cb : 0;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       if constexpr (W4) {
         const int G4 = H >> 7;
-        const size_t rbi = live ? (size_t)m.expert * (2 * I / 16) + m.cb + (rb ? I / 16 : 0) : 0;
+        const size_t rbi = (size_t)ex * (2 * I / 16) + cb + (rb ? I / 16 : 0);
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
           const size_t unit = rbi * G4 + (s0 >> 2) + i;
-          buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + (live ? lane : 0)];
-          sc[rb][i] = a.w4_scales[unit * 16 + lr];
+          buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + lane];
+          sc[rb][i] = a.w4_scales[unit * 16 + r];
         }
       } else {
-        const uint16_t *row;
-        if (!live)
-          row = KIND == 0 ? a.gate_up : a.down;
-        else if (KIND == 0)
-          row = a.gate_up + ((size_t)m.expert * 2 * I + (rb ? I : 0) + m.cb * 16 + r) * H;
+        const uint16_t *base;
+        if (KIND == 0)
+          base = a.gate_up + ((size_t)ex * 2 * I + (rb ? I : 0) + cb * 16) * H + s0 * 32;
         else
-          row = a.down + ((size_t)m.expert * H + m.cb * 32 + rb * 16 + r) * I;
-        row += s0 * 32 + (live ? g * 8 : 0);
+          base = a.down + ((size_t)ex * H + cb * 32 + rb * 16) * I + s0 * 32;
+        const uint8_t *lb = (const uint8_t *)base + lane_a;
 #pragma unroll
-        for (int i = 0; i < AW; ++i) buf[rb][i] = *(const u32x4 *)(row + i * 32);
+        for (int i = 0; i < AW; ++i) buf[rb][i] = *(const u32x4 *)(lb + i * 64);
       }
     }
   };
@@ -181,6 +178,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   load_b(mq[0]);
 
   int u = u_begin;
+  int parity = 0;
   // One unit in ring slot SL; returns whether another unit follows.
   auto step = [&](auto slot_tag) -> bool {
     constexpr int SL = decltype(slot_tag)::value;
@@ -209,7 +207,11 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
       }
     }
 
-    f32x4 *red = s_red + (size_t)(SL & 1) * kWaves * NRB * MT * kWave;
+    // Partial sums alternate between two LDS buffers from step to step (the
+    // epilogue of one unit may still read its buffer while fast waves write
+    // the next unit's partials).
+    f32x4 *red = s_red + (size_t)(parity & 1) * kWaves * NRB * MT * kWave;
+    ++parity;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
@@ -220,28 +222,25 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
 
     // Epilogue of cur: fixed-order sum of the eight K-slices.
     if (KIND == 0) {
-      if (tid < MT * kWave) {
-        const int mt = tid >> 6, l = tid & 63;
+      // One output per thread (4 waves per token block), so no single wave
+      // carries the epilogue's latency into the next unit's barrier.
+      if (tid < MT * 4 * kWave) {
+        const int l = tid & 63, i = (tid >> 6) & 3, mt = tid >> 8;
         const int j = mt * 16 + (l & 15);
-        f32x4 sg = red[(0 * MT + mt) * kWave + l];
-        f32x4 su = red[(1 * MT + mt) * kWave + l];
+        const float *redf = (const float *)red;
+        auto part = [&](int w, int rb) { return redf[(((w * NRB + rb) * MT + mt) * kWave + l) * 4 + i]; };
+        float sg = part(0, 0), su = part(0, 1);
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) {
-          sg += red[((w * NRB + 0) * MT + mt) * kWave + l];
-          su += red[((w * NRB + 1) * MT + mt) * kWave + l];
+          sg += part(w, 0);
+          su += part(w, 1);
         }
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gt = bf16_round(sg[i]);
-          const float up = bf16_round(su[i]);
-          v[i] = gt / (1.0f + expf(-gt)) * up;
-        }
-        u32x2 packed;
-        packed[0] = pack_bf16x2(v[0], v[1]);
-        packed[1] = pack_bf16x2(v[2], v[3]);
+        const float gt = bf16_round(sg);
+        const float up = bf16_round(su);
+        const float v = gt / (1.0f + expf(-gt)) * up;
         if (j < cur.rows)
-          *(u32x2 *)(a.act + (size_t)(cur.row0 + j) * I + cur.cb * 16 + 4 * (l >> 4)) = packed;
+          a.act[(size_t)(cur.row0 + j) * I + cur.cb * 16 + 4 * (l >> 4) + i] =
+              (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
       }
     } else {
       if (tid < NRB * MT * kWave) {
@@ -273,8 +272,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   while (true) {
     if (!step(integral_constant<int, 0>{})) break;
     if (!step(integral_constant<int, 1>{})) break;
-    if constexpr (S == 4) {
+    if constexpr (S >= 3) {
       if (!step(integral_constant<int, 2>{})) break;
+    }
+    if constexpr (S >= 4) {
       if (!step(integral_constant<int, 3>{})) break;
     }
   }
@@ -291,7 +292,10 @@ hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStre
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k, kThreads, lds) !=
             hipSuccess || n < 1)
       n = 1;
-    return n;
+    // Two resident workgroups per CU overlap one's barrier and epilogue with
+    // the other's MFMA phase; a third only adds HBM contention (the bf16
+    // kernels already stream at the practical HBM rate with two).
+    return n < 2 ? n : 2;
   }();
   int grid = num_cus * per_cu;
   if (grid > units_bound) grid = units_bound;
