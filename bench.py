@@ -4,8 +4,9 @@
 
 A step is one full router-inclusive MoE layer forward (router -> planner ->
 gate/up+SwiGLU -> down -> combine) over inputs already resident in HBM,
-replayed from a HIP graph.  Two copies of the weights alternate between steps
-so the 256 MB Infinity Cache cannot serve a step from the previous one.  The
+replayed from HIP graphs of 8 forwards each (BASELINE's timing protocol).  Two
+copies of the weights alternate between forwards so the 256 MB Infinity Cache
+cannot serve a forward from the previous one.  The
 JSON line's ``value`` is tokens/s of ``--workload`` (default: BASELINE
 configs[1], Qwen3-30B-A3B shape, BF16, T=17); ``sweep`` carries every
 BASELINE MoE configuration.  ``roofline`` is the dominant kernel
@@ -81,38 +82,51 @@ def algorithmic(spec, lay, plan):
                 flops=flops, gate_up_flops=4 * t * k * h * inter)
 
 
+FORWARDS_PER_GRAPH = 8
+
+
 def time_layer(plans, steps, warmup):
-    """Average ms per forward over `steps` graph replays (alternating weight copies)."""
-    graphs = []
+    """Average ms per forward over exactly `steps` forwards.  A HIP graph holds
+    FORWARDS_PER_GRAPH forwards that alternate between the weight copies
+    (BASELINE's protocol: graph replays of 8 forwards / 8); a second graph holds
+    the remainder steps % 8.  p50/p95 come from per-replay samples / 8."""
     stream = torch.cuda.Stream()
     for p in plans:
         for _ in range(2):
             p.run()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            p.run()
-        graphs.append(g)
-    for i in range(warmup):
-        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+
+    def capture(n):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n):
+                plans[i % len(plans)].run()
+        return graph
+
+    full = capture(FORWARDS_PER_GRAPH)
+    replays, rem = divmod(steps, FORWARDS_PER_GRAPH)
+    tail = capture(rem) if rem else None
+    for _ in range(max(1, -(-warmup // FORWARDS_PER_GRAPH))):
+        full.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for i in range(steps):
-        graphs[i % len(graphs)].replay()
+    for _ in range(replays):
+        full.replay()
+    if tail is not None:
+        tail.replay()
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    # per-step samples for p50/p95
     samples = []
-    for i in range(min(steps, 40)):
+    for _ in range(20):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        graphs[i % len(graphs)].replay()
+        full.replay()
         b.record()
         b.synchronize()
-        samples.append(a.elapsed_time(b))
-    return total_ms / steps, samples
+        samples.append(a.elapsed_time(b) / FORWARDS_PER_GRAPH)
+    return total_ms / max(steps, 1), samples
 
 
 def time_stage(plans, stage, reps=40):
