@@ -130,20 +130,26 @@ def time_layer(plans, steps, warmup):
 
 
 def time_stage(plans, stage, reps=40):
-    """Average duration (ms) of one launch of `stage`, HIP events on its stream."""
+    """Average duration (ms) of one launch of `stage`: a HIP graph of `reps`
+    back-to-back launches (alternating weight copies) timed with HIP events on
+    the stream the launches run on, so host launch latency is not counted."""
     for p in plans:
         p.run()
     torch.cuda.synchronize()
-    durations = []
-    for i in range(reps):
-        p = plans[i % len(plans)]
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        p.run_stage(stage)
-        b.record()
-        durations.append((a, b))
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(reps):
+            plans[i % len(plans)].run_stage(stage)
+    graph.replay()
     torch.cuda.synchronize()
-    return statistics.mean(a.elapsed_time(b) for a, b in durations)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / reps
 
 
 def measure(name, steps, warmup, device):
@@ -269,6 +275,9 @@ def main():
     ap.add_argument("--workload", default="qwen-bf16-t17", choices=sorted(WORKLOADS))
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only time the segmented-KV GQA attention (BASELINE config 5) and print "
+                         "its records as one JSON line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy 10 times (PMC scaling)")
     args = ap.parse_args()
@@ -283,6 +292,10 @@ def main():
         print("bench.py needs an MI355X", file=sys.stderr)
         sys.exit(1)
     device = torch.device("cuda:0")
+    if args.attention_only:
+        print(json.dumps({"attention": [measure_attention(t, device) for t in (32, 96, 256)]}),
+              flush=True)
+        return
     log(f"[bench] workload {args.workload}")
     main_res, lay, plans = measure(args.workload, args.steps, args.warmup, device)
     spec = WORKLOADS[args.workload]

@@ -229,3 +229,33 @@ def test_gqa_reference_matches_manual_softmax():
             sc = (keys[:n_vis, kv] @ q[i, h]) / math.sqrt(d)
             p = torch.softmax(sc, 0)
             assert torch.allclose(out[i, h], p @ vals[:n_vis, kv], atol=1e-5)
+
+
+def test_gqa_reference_closed_forms():
+    """Zero keys give uniform weights over the visible keys (history + causal prefix);
+    query 0 of an empty history sees exactly one key; KV head j of constant value j
+    shows the head mapping h // (Hq / Hkv)."""
+    g = torch.Generator().manual_seed(1)
+    t, hq, hkv, d = 5, 8, 2, 16
+    q = torch.randn((t, hq, d), generator=g)
+    lens = (3, 0, 2, t)
+    segs = [(torch.zeros((L, hkv, d)), torch.randn((L, hkv, d), generator=g)) for L in lens]
+    out = O.gqa_segmented_reference(q, segs)
+    vals = torch.cat([v for _, v in segs])
+    hist = sum(lens[:-1])
+    for i in range(t):
+        for h in range(hq):
+            mean = vals[:hist + i + 1, h // (hq // hkv)].mean(0)
+            assert torch.allclose(out[i, h], mean, atol=1e-6)
+    # single visible key: the output is that key's value row exactly.
+    one = [(torch.randn((t, hkv, d), generator=g), torch.randn((t, hkv, d), generator=g))]
+    out1 = O.gqa_segmented_reference(q, one)
+    for h in range(hq):
+        assert torch.equal(out1[0, h], one[0][1][0, h // (hq // hkv)])
+    # head mapping: KV head j holds the constant j in every value.
+    const = [(torch.randn((L, hkv, d), generator=g),
+              torch.arange(hkv, dtype=torch.float32).view(1, hkv, 1).expand(L, hkv, d).clone())
+             for L in lens]
+    out2 = O.gqa_segmented_reference(q, const)
+    for h in range(hq):
+        assert torch.allclose(out2[:, h], torch.full((t, d), float(h // (hq // hkv))), atol=1e-6)
