@@ -48,6 +48,11 @@ __device__ __forceinline__ int swz(int row, int c) {
   else return row * 256 + ((c ^ (row & 15)) << 4);
 }
 
+#ifndef MOE_TILE_TASK_BLOCK
+#define MOE_TILE_TASK_BLOCK 4
+#endif
+constexpr int kTaskBlock = MOE_TILE_TASK_BLOCK;
+
 template <int KIND, bool W4>
 struct TileCfg {
   static constexpr int BN = (KIND == 0 && W4) ? 128 : 256;  // weight rows per tile
@@ -85,8 +90,15 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
   const int slot = (G % 8) ? (int)blockIdx.x : (int)(blockIdx.x / 8 + (blockIdx.x % 8) * (G / 8));
 
   for (int u = slot; u < total; u += G) {
-    const int nt = u / num_tasks;
-    const int t = u - nt * num_tasks;
+    // Units come in blocks of kTaskBlock consecutive tasks (the task list is
+    // expert-major), column-tile-major within a block: a block's tasks share
+    // each weight tile of their expert, and the block's token rows stay in
+    // the one L2 that runs the block for all of its column tiles.
+    const int blk = u / (kTaskBlock * ntiles);
+    const int rem = u - blk * (kTaskBlock * ntiles);
+    const int mb = min(kTaskBlock, num_tasks - blk * kTaskBlock);
+    const int nt = rem / mb;
+    const int t = blk * kTaskBlock + (rem - nt * mb);
     const int e = tasks[4 * t], row0 = tasks[4 * t + 1], rows = tasks[4 * t + 2];
 
     // --- per-lane global sources of this unit -------------------------------
