@@ -127,7 +127,13 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(const uint32_t *__restr
 
 hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
                           int path, int num_cus, hipStream_t s) {
-  if (path == kTile) return launch_tile_gate_up(a, task_capacity, w4, num_cus, s);
+  // W4 with several rows per expert, and every 64-row task: decode each weight
+  // fragment once for up to 64 token rows (one unit per wave).  With about one
+  // row per expert the split-K streaming kernel overlaps the decode better.
+  if (w4 && path != kGeneric && (token_block == 64 || (long long)a.R >= 4LL * a.E) &&
+      wave_w4_shape_ok(a.H, a.I, token_block))
+    return launch_wave_w4_gate_up(a, task_capacity, token_block, s);
+  if (path == kTile) return w4 ? hipErrorInvalidValue : launch_tile_gate_up(a, task_capacity, num_cus, s);
   if (path == kStream) return launch_stream_gate_up(a, task_capacity, token_block, w4, num_cus, s);
   if (w4) return hipErrorInvalidValue;
   const dim3 grid(task_capacity, (token_block * a.I + 255) / 256);

@@ -55,7 +55,12 @@ hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int tok
 hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,
                               int num_cus, hipStream_t s);
 bool stream_shape_ok(int H, int I, bool w4);
-hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, bool w4, int num_cus,
+// W4 gate/up + SwiGLU, one unit per wave with K-chunked token rows in LDS, for
+// tasks with several rows per expert (token_block 16, 32 or 64).
+bool wave_w4_shape_ok(int H, int I, int token_block);
+hipError_t launch_wave_w4_gate_up(const ExpertArgs &a, int task_capacity, int token_block,
+                                  hipStream_t s);
+hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, int num_cus,
                                hipStream_t s);
 hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s);
 bool tile_shape_ok(int H, int I, bool w4);

@@ -61,7 +61,6 @@ __device__ __forceinline__ void lds_barrier() {
 template <int KIND, int MT, int SPW, bool W4>
 __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   constexpr int NRB = 2;
-  constexpr int ROWS = 16 * MT;
   extern __shared__ f32x4 s_red[];  // [2][kWaves][NRB][MT][64]
 
   const int tid = threadIdx.x;
@@ -81,7 +80,6 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   if (u_begin >= total) return;
 
   const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
-  const MOE_CONST int32_t *row_idx = as_const(KIND == 0 ? a.row_token : a.row_route);
 
   // Unit metadata: scalars, plus one VGPR whose lane k < ROWS holds the
   // token (gate/up) or route (down) of the task's row k (one vector load; the

@@ -12,8 +12,9 @@
 // and token tile [BM][BK] are loaded global -> registers (two stages in
 // flight) -> LDS, 16-byte chunks XOR-swizzled by row so that the MFMA
 // operand reads are bank-conflict free, then 8 waves (4 along N x 2 along M)
-// run 16x16x32 bf16 MFMAs.  W4G128 weights are decoded once into the bf16 LDS
-// tile with w4_decode8 (bit-exact dequantisation) and reused by all BM rows.
+// run 16x16x32 bf16 MFMAs.  (W4G128 gate/up with many rows per expert runs in
+// the wave kernel of moe_wave.hip, which decodes each weight once into MFMA
+// registers; the down weights are bf16 in both formats.)
 //
 // Epilogues match the streaming kernels: gate/up round to bf16, SwiGLU in
 // fp32, bf16 act rows; down rounds to bf16 and scatters rows to route order.
@@ -53,22 +54,22 @@ __device__ __forceinline__ int swz(int row, int c) {
 #endif
 constexpr int kTaskBlock = MOE_TILE_TASK_BLOCK;
 
-template <int KIND, bool W4>
+template <int KIND>
 struct TileCfg {
-  static constexpr int BN = (KIND == 0 && W4) ? 128 : 256;  // weight rows per tile
-  static constexpr int BK = W4 ? 128 : 64;
+  static constexpr int BN = 256;  // weight rows per tile
+  static constexpr int BK = 64;
   static constexpr int WNT = BN / 4 / 16;                   // 16-row tiles per wave
   static constexpr int A_BYTES = BN * BK * 2;
   static constexpr int B_BYTES = BM * BK * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int A_LOADS = W4 ? 1 : A_BYTES / 1024 / kWaves;  // 16-B loads per lane
+  static constexpr int A_LOADS = A_BYTES / 1024 / kWaves;  // 16-B loads per lane
   static constexpr int B_LOADS = B_BYTES / 1024 / kWaves;
   static constexpr int OUT_COLS = KIND == 0 ? BN / 2 : BN;  // output columns per n-tile
 };
 
-template <int KIND, bool W4>
+template <int KIND>
 __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
-  using C = TileCfg<KIND, W4>;
+  using C = TileCfg<KIND>;
   constexpr int BN = C::BN, BK = C::BK, WNT = C::WNT;
   constexpr int KS = BK / 32;  // MFMA k-steps per stage
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
     const int e = tasks[4 * t], row0 = tasks[4 * t + 1], rows = tasks[4 * t + 2];
 
     // --- per-lane global sources of this unit -------------------------------
-    // Token tile rows: bf16 path rows = 8 per 1 KB load (64-K), W4 path 4 (128-K).
+    // Token tile rows: 8 rows per 1 KB load (64-K stages).
     constexpr int B_RPL = 1024 / (BK * 2);  // rows per 1 KB
     const uint16_t *bsrc[C::B_LOADS];
     int brow[C::B_LOADS];
@@ -118,59 +119,33 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
     }
     const uint16_t *asrc[C::A_LOADS];
     int arow[C::A_LOADS];
-    const u32x4 *wsrc = nullptr;
-    const uint16_t *ssrc = nullptr;
-    if constexpr (W4) {
-      // Wave w decodes row block w (16 rows) of the 128-row tile.
-      const int G4 = H >> 7;
-      const int half = wave >> 2;  // 0: gate rows, 1: up rows
-      const size_t rb = (size_t)e * (2 * I / 16) + (half ? I / 16 : 0) + (nt * 64 + (wave & 3) * 16) / 16;
-      wsrc = (const u32x4 *)a.w4_words + rb * G4 * 64 + lane;
-      ssrc = a.w4_scales + rb * G4 * 16 + (lane & 15);
-    } else {
 #pragma unroll
-      for (int i = 0; i < C::A_LOADS; ++i) {
-        const int row = (wave * C::A_LOADS + i) * 8 + lane / 8;  // tile row
-        arow[i] = row;
-        size_t wrow;
-        if (KIND == 0)
-          wrow = (size_t)e * 2 * I + (row < BN / 2 ? nt * (BN / 2) + row : I + nt * (BN / 2) + row - BN / 2);
-        else
-          wrow = (size_t)e * H + nt * BN + row;
-        asrc[i] = (KIND == 0 ? a.gate_up : a.down) + wrow * Kdim + (lane % 8) * 8;
-      }
+    for (int i = 0; i < C::A_LOADS; ++i) {
+      const int row = (wave * C::A_LOADS + i) * 8 + lane / 8;  // tile row
+      arow[i] = row;
+      size_t wrow;
+      if (KIND == 0)
+        wrow = (size_t)e * 2 * I + (row < BN / 2 ? nt * (BN / 2) + row : I + nt * (BN / 2) + row - BN / 2);
+      else
+        wrow = (size_t)e * H + nt * BN + row;
+      asrc[i] = (KIND == 0 ? a.gate_up : a.down) + wrow * Kdim + (lane % 8) * 8;
     }
 
     // --- register stage sets ---------------------------------------------
     struct Regs {
-      u32x4 a[W4 ? 1 : C::A_LOADS];
-      uint32_t s;
+      u32x4 a[C::A_LOADS];
       u32x4 b[C::B_LOADS];
     };
     auto gload = [&](Regs &R, int kt) {
-      if constexpr (W4) {
-        R.a[0] = wsrc[(size_t)kt * 64];
-        R.s = ssrc[kt * 16];
-      } else {
 #pragma unroll
-        for (int i = 0; i < C::A_LOADS; ++i) R.a[i] = *(const u32x4 *)(asrc[i] + kt * BK);
-      }
+      for (int i = 0; i < C::A_LOADS; ++i) R.a[i] = *(const u32x4 *)(asrc[i] + kt * BK);
 #pragma unroll
       for (int i = 0; i < C::B_LOADS; ++i) R.b[i] = *(const u32x4 *)(bsrc[i] + kt * BK);
     };
     auto sts = [&](uint8_t *buf, const Regs &R) {
       uint8_t *abuf = buf, *bbuf = buf + C::A_BYTES;
-      if constexpr (W4) {
-        const W4Scale ks = w4_scale(bf16_bits_to_f32(R.s));
-        const int row = wave * 16 + (lane & 15);
-        const int g = lane >> 4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *(u32x4 *)(abuf + swz<BK>(row, 4 * j + g)) = w4_decode8(R.a[0][j], ks);
-      } else {
-#pragma unroll
-        for (int i = 0; i < C::A_LOADS; ++i) *(u32x4 *)(abuf + swz<BK>(arow[i], lane % 8)) = R.a[i];
-      }
+      for (int i = 0; i < C::A_LOADS; ++i) *(u32x4 *)(abuf + swz<BK>(arow[i], lane % 8)) = R.a[i];
 #pragma unroll
       for (int i = 0; i < C::B_LOADS; ++i)
         *(u32x4 *)(bbuf + swz<BK>(brow[i], lane % (BK / 8))) = R.b[i];
@@ -263,10 +238,10 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
   }
 }
 
-template <int KIND, bool W4>
+template <int KIND>
 hipError_t launch_tile_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
-  using C = TileCfg<KIND, W4>;
-  auto k = tile_kernel<KIND, W4>;
+  using C = TileCfg<KIND>;
+  auto k = tile_kernel<KIND>;
   const size_t lds = 2 * (size_t)C::STAGE_BYTES;
   static int per_cu = [&] {
     int n = 1;
@@ -287,23 +262,19 @@ hipError_t launch_tile_one(const ExpertArgs &a, int units_bound, int num_cus, hi
 }  // namespace
 
 bool tile_shape_ok(int H, int I, bool w4) {
-  // gate/up: K = H in BK stages (even count), act columns in BN/2 tiles;
-  // down: K = I in 64-wide stages (even count), H in 256-row tiles.
-  const int bk_gu = w4 ? 128 : 64;
-  if (H % (2 * bk_gu) || I % 128) return false;
-  if (I % (w4 ? 64 : 128)) return false;
-  if (H % 256) return false;
-  return true;
+  // down (both formats): K = I in 64-wide stages (even count), H in 256-row tiles.
+  if (I % 128 || H % 256) return false;
+  // gate/up: bf16 here, K = H in 64-wide stages (even count), act columns in
+  // 128-column tiles; W4 in the wave kernel.
+  return w4 ? wave_w4_shape_ok(H, I, 64) : H % 128 == 0;
 }
 
-hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, bool w4, int num_cus,
-                               hipStream_t s) {
-  if (w4) return launch_tile_one<0, true>(a, task_capacity * (a.I / 64), num_cus, s);
-  return launch_tile_one<0, false>(a, task_capacity * (a.I / 128), num_cus, s);
+hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
+  return launch_tile_one<0>(a, task_capacity * (a.I / 128), num_cus, s);
 }
 
 hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
-  return launch_tile_one<1, false>(a, task_capacity * (a.H / 256), num_cus, s);
+  return launch_tile_one<1>(a, task_capacity * (a.H / 256), num_cus, s);
 }
 
 }  // namespace moe

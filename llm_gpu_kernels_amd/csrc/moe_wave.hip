@@ -1,0 +1,236 @@
+// W4A16 gate/up + SwiGLU for tasks with several rows per expert on gfx950
+// (reference: cuda_gate_up_w4_sync, cuda_w4_gate_up.cu:46-100; semantics of
+// _dynamic_grouped_gate_up_swiglu, moe_fused.py:18-73).
+//
+// Unit = (task, 16 intermediate columns): 16 gate + 16 up weight rows against
+// the task's 16*MT token rows.  One unit per wave over the whole K:
+//
+//  * The int4 weights stream from HBM straight into MFMA A registers (one
+//    16-byte load per lane = 32 int4 of one row = a whole 128-K group, from
+//    the tiled layout where each such load is 1 KiB contiguous) through a
+//    ring of D4 groups, and each fragment is decoded once (w4_decode8,
+//    bit-exact with the reference dequantisation) and used by MT MFMAs: at
+//    MT = 4 the decode and the matrix cores carry comparable work instead of
+//    the decode being paid once per 16 tokens.
+//  * A workgroup = one task and 8 adjacent column blocks (8 waves).  The
+//    task's token rows (MFMA B operand, gathered through the route list) are
+//    staged in LDS in K-chunks of 32 KiB, double buffered: the next chunk is
+//    loaded into registers while the current one is multiplied, so the only
+//    workgroup barrier is one per chunk.  64 KiB of LDS per workgroup and at
+//    most 128 VGPRs keep two workgroups per CU.
+//  * The epilogue is in-wave (gate and up of a (feature, token) sit in the
+//    same lane) with the reference's rounding stages.
+#include <type_traits>
+
+#include "common.h"
+#include "moe_internal.h"
+
+#define MOE_CONST __attribute__((address_space(4)))
+
+namespace moe {
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int D4 = 2;                    // int4 groups in flight per wave (ring slots)
+constexpr int kChunkBytes = 32 * 1024;   // one B buffer
+
+template <typename T>
+__device__ __forceinline__ const MOE_CONST T *as_const(const T *p) {
+  return (const MOE_CONST T *)p;
+}
+
+// Calls f(integral_constant<int, d>) for d = 0, 1, ... in order.
+template <class F, int... d>
+__device__ __forceinline__ void unroll_seq(F &&f, std::integer_sequence<int, d...>) {
+  (f(std::integral_constant<int, d>{}), ...);
+}
+
+// Byte offset of 16-byte chunk c of row `row` in a staged [rows][KC] chunk.
+template <int KC>
+__device__ __forceinline__ uint32_t b_off(int row, int c) {
+  return (uint32_t)row * (KC * 2) + (uint32_t)((c ^ (row & 15)) << 4);
+}
+
+// MT = 1, 2: at most 128 VGPRs (4 waves per SIMD, two workgroups per CU): the
+// decode is VALU-bound and one wave issues a VALU op only every few cycles.
+// MT = 4 does four MFMAs per decoded fragment and keeps 2 waves per SIMD.
+template <int MT>
+__global__ __launch_bounds__(kThreads, 4) void wave_w4_kernel(ExpertArgs a) {
+  constexpr int NRB = 2;
+  constexpr int ROWS = 16 * MT;
+  constexpr int KC = kChunkBytes / (ROWS * 2);  // K per chunk: 1024, 512, 256
+  constexpr int GPC = KC / 128;                 // int4 groups per chunk: 8, 4, 2
+  constexpr int BPT = kChunkBytes / 16 / kThreads;  // 16-byte B pieces per thread per chunk
+  static_assert(GPC % D4 == 0, "a chunk holds whole ring rounds");
+  __shared__ __attribute__((aligned(16))) uint8_t s_b[2][kChunkBytes];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & (kWave - 1);
+  const int r = lane & 15, g = lane >> 4;
+  const int H = a.H, I = a.I;
+  const int nunits = I / 16;
+  const int groups = (nunits + kWaves - 1) / kWaves;
+  const int task = blockIdx.x / groups;
+  if (task >= *as_const(a.num_tasks)) return;
+  const int unit = (blockIdx.x - task * groups) * kWaves + wave;
+  const bool active = unit < nunits;
+  const int cb = active ? unit : 0;
+
+  const MOE_CONST int32_t *tk = as_const((const int32_t *)a.tasks) + 4 * task;
+  const int expert = tk[0], row0 = tk[1], rows = tk[2];
+
+  // ---- weight ring (A operand) ---------------------------------------------
+  const int NS = H >> 7;  // int4 groups along K
+  size_t rbi[NRB];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb)
+    rbi[rb] = ((size_t)expert * (2 * I / 16) + cb + (rb ? I / 16 : 0)) * NS;
+  u32x4 ring[D4][NRB];
+  uint32_t sring[D4][NRB];
+  auto load_group = [&](int s, u32x4 (&slot)[NRB], uint32_t (&sslot)[NRB])
+                        __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      const size_t u = rbi[rb] + s;
+      slot[rb] = ((const u32x4 *)a.w4_words)[u * kWave + lane];
+      sslot[rb] = a.w4_scales[u * 16 + r];
+    }
+  };
+  if (active) {
+#pragma unroll
+    for (int d = 0; d < D4; ++d) load_group(d, ring[d], sring[d]);
+  }
+
+  // ---- token rows (B operand), K-chunked and double buffered ---------------
+  // Thread piece i covers row (i*512 + tid) / (KC/8), 16-byte chunk
+  // (i*512 + tid) % (KC/8) of every K-chunk; rows past the task's end load
+  // row 0 (finite data in columns the epilogue never stores).
+  const uint16_t *bsrc[BPT];
+  uint32_t bdst[BPT];
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    const int idx = i * kThreads + tid;
+    const int row = idx / (KC / 8), c = idx % (KC / 8);
+    const int rr = row < rows ? row : 0;
+    bsrc[i] = a.x + (size_t)a.row_token[row0 + rr] * H + 8 * c;
+    bdst[i] = b_off<KC>(row, c);
+  }
+  u32x4 breg[BPT];
+  auto bload = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) breg[i] = *(const u32x4 *)(bsrc[i] + (size_t)c * KC);
+  };
+  auto bstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) *(u32x4 *)(s_b[buf] + bdst[i]) = breg[i];
+  };
+
+  const int NCH = H / KC;
+  bload(0);
+  bstore(0);
+  if (NCH > 1) bload(1);
+  __syncthreads();
+
+  f32x4 acc[NRB][MT];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Group s (ring slot d) against chunk buffer `buf`, whose first group is s0c.
+  auto step = [&](int s, auto d_tag, int buf, int s0c) __attribute__((always_inline)) {
+    constexpr int d = decltype(d_tag)::value;
+    const uint8_t *bb = s_b[buf];
+    // Both row blocks (gate, up) are decoded before the token fragments are
+    // read, so each B fragment comes out of LDS once for two MFMAs.
+    const W4Scale ks0 = w4_scale(bf16_bits_to_f32(sring[d][0]));
+    const W4Scale ks1 = w4_scale(bf16_bits_to_f32(sring[d][1]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 af0 = w4_decode8(ring[d][0][j], ks0);
+      const u32x4 af1 = w4_decode8(ring[d][1][j], ks1);
+      const int c = 4 * (4 * (s - s0c) + j) + g;  // 16-byte chunk of k-step within the chunk
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 bf = *(const u32x4 *)(bb + b_off<KC>(mt * 16 + r, c));
+        acc[0][mt] = mfma16(af0, bf, acc[0][mt]);
+        acc[1][mt] = mfma16(af1, bf, acc[1][mt]);
+      }
+    }
+    if (s + D4 < NS) load_group(s + D4, ring[d], sring[d]);
+  };
+  using std::integral_constant;
+  // One ring round = D4 consecutive groups in slots 0 .. D4-1, starting at
+  // group s0 (a multiple of D4) of the chunk that starts at group s0c.
+  auto ring_round = [&](int s0, int buf, int s0c) __attribute__((always_inline)) {
+    unroll_seq([&](auto dt) __attribute__((always_inline)) {
+      step(s0 + decltype(dt)::value, dt, buf, s0c);
+    }, std::make_integer_sequence<int, D4>{});
+  };
+  for (int c = 0; c < NCH; ++c) {
+    const int buf = c & 1;
+    if (active) {
+      const int s0c = c * GPC;
+#pragma unroll
+      for (int q = 0; q < GPC / D4; ++q) ring_round(s0c + q * D4, buf, s0c);
+    }
+    // Stage chunk c+1 (already in registers) into the other buffer, whose last
+    // readers (chunk c-1) passed the previous barrier; then request chunk c+2.
+    if (c + 1 < NCH) bstore(buf ^ 1);
+    __syncthreads();
+    if (c + 2 < NCH) bload(c + 2);
+  }
+  if (!active) return;
+
+  // ---- epilogue: lane holds features 4g + i of token row mt*16 + r ---------
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int j = mt * 16 + r;
+    if (j >= rows) continue;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float gt = bf16_round(acc[0][mt][i]);
+      const float up = bf16_round(acc[1][mt][i]);
+      v[i] = gt / (1.0f + expf(-gt)) * up;
+    }
+    u32x2 packed;
+    packed[0] = pack_bf16x2(v[0], v[1]);
+    packed[1] = pack_bf16x2(v[2], v[3]);
+    *(u32x2 *)(a.act + (size_t)(row0 + j) * I + cb * 16 + 4 * g) = packed;
+  }
+}
+
+template <int MT>
+hipError_t launch_mt(const ExpertArgs &a, int task_capacity, hipStream_t s) {
+  const int groups = (a.I / 16 + kWaves - 1) / kWaves;
+  const long long grid = (long long)task_capacity * groups;
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL(wave_w4_kernel<MT>, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// K-chunks are 1024 / 512 / 256 wide for 16 / 32 / 64-row tasks (whole ring
+// rounds each); H must hold whole chunks.
+bool wave_w4_shape_ok(int H, int I, int token_block) {
+  if (token_block != 16 && token_block != 32 && token_block != 64) return false;
+  const int kc = kChunkBytes / (token_block * 2);
+  return I > 0 && I % 16 == 0 && H % kc == 0;
+}
+
+hipError_t launch_wave_w4_gate_up(const ExpertArgs &a, int task_capacity, int token_block,
+                                  hipStream_t s) {
+  switch (token_block) {
+    case 16: return launch_mt<1>(a, task_capacity, s);
+    case 32: return launch_mt<2>(a, task_capacity, s);
+    case 64: return launch_mt<4>(a, task_capacity, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace moe
