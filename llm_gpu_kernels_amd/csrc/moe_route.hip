@@ -153,7 +153,10 @@ static_assert(16 * 32 <= kLdsRoutes, "fused router (T <= 16, K <= 32) must fit t
 // LDS of the planner, carved by hand so the route arrays exist only when the
 // routes fit (R <= kLdsRoutes).
 struct PlanShared {
-  int wcnt[kPlanWaves][kMaxExperts];
+  // Per-round per-wave expert counts, turned into exclusive prefixes in place;
+  // two tables by round parity so the next round's table is cleared while the
+  // current one is read.
+  int wcnt[2][kPlanWaves][kMaxExperts];
   int run[kMaxExperts];
   int off[kMaxExperts];
   int toff[kMaxExperts + 1];
@@ -174,6 +177,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   const int E = a.E;
   if (tid == 0) sh.status = 0;
   for (int e = tid; e < E; e += kPlanThreads) sh.run[e] = 0;
+  for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) (&sh.wcnt[0][0][0])[i] = 0;
   uint32_t flags = 0;
 
   bool ids_in_lds = false;
@@ -205,18 +209,12 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
     if (LDSR && ids_in_lds) return s_ids[q];
     return (long long)ids[q];
   };
-  // Pass 1: canonical ranks, 1024 routes per round.
-  for (int base = 0; base < a.R; base += kPlanThreads) {
-    for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) (&sh.wcnt[0][0])[i] = 0;
-    __syncthreads();
-    const int q = base + tid;
+  // Pass 1: canonical ranks, 1024 routes per round, two barriers per round.
+  auto rank_round = [&](int r, long long idv, float wv) __attribute__((always_inline)) {
+    int (*cnt)[kMaxExperts] = sh.wcnt[r & 1];
+    int *next = &sh.wcnt[(r + 1) & 1][0][0];
+    const int q = r * kPlanThreads + tid;
     const bool valid = q < a.R;
-    long long idv = -1;
-    float wv = 0.f;
-    if (valid) {
-      idv = id_of(q);
-      wv = (LDSR && ids_in_lds) ? s_w[q] : a.weights[q];
-    }
     const bool ok = valid && idv >= 0 && idv < E;
     if (valid && !ok) flags |= 1u;
     if (valid && !isfinite(wv)) flags |= 2u;
@@ -229,13 +227,23 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
       match &= set ? b : ~b;
     }
     const int lrank = __popcll(match & lanemask_lt());
-    if (ok && lrank == 0) sh.wcnt[wave][id] = __popcll(match);
+    if (ok && lrank == 0) cnt[wave][id] = __popcll(match);
     __syncthreads();
-    int rank = -1;
-    if (ok) {
-      rank = sh.run[id] + lrank;
-      for (int w = 0; w < wave; ++w) rank += sh.wcnt[w][id];
+    // Counts -> exclusive prefixes over (earlier rounds, earlier waves); the
+    // other table, last read before this round's first barrier, is cleared.
+    for (int e = tid; e < E; e += kPlanThreads) {
+      int c = sh.run[e];
+#pragma unroll
+      for (int w = 0; w < kPlanWaves; ++w) {
+        const int t = cnt[w][e];
+        cnt[w][e] = c;
+        c += t;
+      }
+      sh.run[e] = c;
     }
+    for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) next[i] = 0;
+    __syncthreads();
+    const int rank = ok ? cnt[wave][id] + lrank : -1;
     if (valid) {
       a.ranks[q] = rank;
       if (LDSR) {
@@ -243,13 +251,33 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
         if (!ids_in_lds) s_ids[q] = ok ? id : -1;
       }
     }
-    __syncthreads();
-    for (int e = tid; e < E; e += kPlanThreads) {
-      int c = 0;
-      for (int w = 0; w < kPlanWaves; ++w) c += sh.wcnt[w][e];
-      sh.run[e] += c;
+  };
+  if constexpr (LDSR) {
+    // Every round's id and weight are requested before the first round, so
+    // the rounds do not each wait a memory round trip after their barrier.
+    constexpr int kRounds = kLdsRoutes / kPlanThreads;
+    long long pid[kRounds];
+    float pw[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int q = r * kPlanThreads + tid;
+      pid[r] = -1;
+      pw[r] = 0.f;
+      if (q < a.R) {
+        pid[r] = id_of(q);
+        pw[r] = ids_in_lds ? s_w[q] : a.weights[q];
+      }
     }
-    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      if (r * kPlanThreads >= a.R) break;
+      rank_round(r, pid[r], pw[r]);
+    }
+  } else {
+    for (int r = 0; r * kPlanThreads < a.R; ++r) {
+      const int q = r * kPlanThreads + tid;
+      rank_round(r, q < a.R ? id_of(q) : -1, q < a.R ? a.weights[q] : 0.f);
+    }
   }
 
   // Pass 2: exclusive scans of counts and of per-expert task counts (wave 0,
