@@ -156,6 +156,33 @@ def test_routed_w4_layer(tokens, gpu_device):
     _routed_parity("qwen", tokens, "uniform", gpu_device, w4=True)
 
 
+@pytest.mark.parametrize("tokens", [17, 193])
+def test_w4_token_blocks(tokens, gpu_device):
+    """W4 gate/up with 16-, 32- and 64-row tasks: at T=17 the split-K streaming kernel
+    (16, 32 rows) and the one-unit-per-wave kernel (64 rows); at T=193 the wave kernel
+    with 1, 2 and 4 token blocks per fragment.  Each within tolerance of the FP32
+    oracle on the dequantised weights, and of the 16-row result."""
+    lay = make_layer("qwen", tokens, seed=5, device=gpu_device)
+    ids, w = O.route_topk(lay["logits"].cpu(), 8)
+    packed = quantize_gate_up(lay["gate_up"].cpu())
+    tiled = tile_gate_up(packed).to(gpu_device)
+    ref = O.moe_reference(lay["x"].cpu(), O.dequantize_w4(packed.words, packed.scales),
+                          lay["down"].cpu(), ids, w)
+    outs = {}
+    for bm in (16, 32, 64):
+        plan = prepare_w4_moe(lay["x"], tiled, lay["down"], ids.to(gpu_device), w.to(gpu_device),
+                              down_config=GemmConfig(block_m=bm))
+        assert plan.layout.token_block == bm
+        out = plan.run().clone()
+        torch.cuda.synchronize()
+        m = O.error(out, ref)
+        assert m["passed"], (bm, m)
+        outs[bm] = out
+    for bm in (32, 64):
+        m = O.error(outs[bm], outs[16].float().cpu())
+        assert m["passed"], (bm, m)
+
+
 def test_status_bits(gpu_device):
     x, gu, dn, ids, rw = O.make_inputs(tokens=3, experts=4, topk=2, hidden=128, intermediate=128,
                                        id_dtype=torch.int32, pattern="random", seed=101)
