@@ -20,6 +20,8 @@ namespace moe {
 namespace {
 
 // out[t] = bf16(sum_s fp32(routed[t*K+s]) * w[t,s]), slot order, no FMA.
+// Slots are taken eight at a time with every load of a chunk issued before
+// the first add, so a token costs one memory round trip per eight slots.
 __global__ __launch_bounds__(256) void combine_kernel(ExpertArgs a) {
   const int t = blockIdx.x;
   const int h = (blockIdx.y * 256 + threadIdx.x) * 8;
@@ -27,17 +29,30 @@ __global__ __launch_bounds__(256) void combine_kernel(ExpertArgs a) {
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int s = 0; s < a.K; ++s) {
-    const int q = t * a.K + s;
-    if (a.map[q] < 0) continue;
-    const float w = a.weights[q];
-    const u32x4 v = *(const u32x4 *)(a.routed + (size_t)q * a.H + h);
+  for (int s0 = 0; s0 < a.K; s0 += 8) {
+    int mp[8];
+    float wt[8];
+    u32x4 v[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lo = bf16_bits_to_f32(v[i] & 0xffffu);
-      const float hi = bf16_bits_to_f32(v[i] >> 16);
-      acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(lo, w));
-      acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(hi, w));
+    for (int s = 0; s < 8; ++s) {
+      const int q = t * a.K + s0 + s;
+      const bool in = s0 + s < a.K;
+      mp[s] = in ? a.map[q] : -1;
+      wt[s] = in ? a.weights[q] : 0.f;
+      // Every route's row is read (in bounds); a dropped route's row is
+      // never added, whatever it holds.
+      v[s] = *(const u32x4 *)(a.routed + (size_t)(in ? q : t * a.K) * a.H + h);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (mp[s] < 0) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = bf16_bits_to_f32(v[s][i] & 0xffffu);
+        const float hi = bf16_bits_to_f32(v[s][i] >> 16);
+        acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(lo, wt[s]));
+        acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(hi, wt[s]));
+      }
     }
   }
   u32x4 o;
