@@ -238,6 +238,237 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
   }
 }
 
+// ---- warp-specialised variant ------------------------------------------------
+// The same units, tiles and MFMA work, with the K stages moved by global ->
+// LDS direct loads (16 bytes per lane, gfx950) into a ring of kWsStages LDS
+// stages, kWsStages - 1 stages ahead of the matrix cores.  Four loader waves
+// issue every load and carry every vector-memory wait; the eight MFMA waves
+// only read LDS.  One workgroup barrier per stage publishes that stage (the
+// loaders waited for it) and frees the oldest buffer (every MFMA wave has
+// finished reading it).  One 768-thread workgroup per CU owns all 160 KB of
+// LDS.
+constexpr int kWsConsumers = 8;
+constexpr int kWsLoaders = 4;
+constexpr int kWsThreads = (kWsConsumers + kWsLoaders) * 64;
+constexpr int kWsStages = 4;
+
+// s_waitcnt with only the vector-memory counter bounded (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kWsThreads) void tile_ws_kernel(ExpertArgs a) {
+  using C = TileCfg<KIND>;
+  constexpr int BN = C::BN, BK = C::BK, WNT = C::WNT;
+  constexpr int KS = BK / 32;
+  static_assert(BK == 64, "one 128-byte row piece per stage");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int H = a.H, I = a.I;
+  const int Kdim = KIND == 0 ? H : I;
+  const int KT = Kdim / BK;
+  const int ntiles = (KIND == 0 ? I : H) / C::OUT_COLS;
+  const int num_tasks = *as_const(a.num_tasks);
+  const int total = num_tasks * ntiles;
+  const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
+  const int G = gridDim.x;
+  const int slot = (G % 8) ? (int)blockIdx.x : (int)(blockIdx.x / 8 + (blockIdx.x % 8) * (G / 8));
+  const int nu = slot < total ? (total - slot + G - 1) / G : 0;
+  const int nstages = nu * KT;
+
+  // Unit i of this workgroup (same order and task blocks as tile_kernel).
+  struct Unit {
+    int e, row0, rows, nt;
+  };
+  auto unit_of = [&](int i) {
+    const int u = slot + i * G;
+    const int blk = u / (kTaskBlock * ntiles);
+    const int rem = u - blk * (kTaskBlock * ntiles);
+    const int mb = min(kTaskBlock, num_tasks - blk * kTaskBlock);
+    Unit un;
+    un.nt = rem / mb;
+    const int t = blk * kTaskBlock + (rem - un.nt * mb);
+    un.e = tasks[4 * t];
+    un.row0 = tasks[4 * t + 1];
+    un.rows = tasks[4 * t + 2];
+    return un;
+  };
+
+  if (wave >= kWsConsumers) {
+    // ---- loaders: wave lw moves tile rows [lw*64, +64) of the weights and
+    // [lw*16, +16) of the tokens, 8 rows (1 KiB of LDS) per instruction.
+    const int lw = wave - kWsConsumers;
+    constexpr int A_PER = BN / kWsLoaders / 8;
+    constexpr int B_PER = BM / kWsLoaders / 8;
+    constexpr int PER = A_PER + B_PER;  // instructions per stage per loader wave
+    static_assert(kWsStages == 4 && 2 * PER < 64, "wait counts below assume 4 stages");
+    const uint16_t *asrc[A_PER];
+    const uint16_t *bsrc[B_PER];
+    int cur = -1;
+    auto setup = [&](int i) {
+      const Unit un = unit_of(i);
+#pragma unroll
+      for (int j = 0; j < A_PER; ++j) {
+        const int row = lw * (BN / kWsLoaders) + j * 8 + lane / 8;  // tile row
+        const int c = (lane % 8) ^ ((row >> 1) & 7);  // logical chunk of LDS chunk lane%8
+        size_t wrow;
+        if (KIND == 0)
+          wrow = (size_t)un.e * 2 * I +
+                 (row < BN / 2 ? un.nt * (BN / 2) + row : I + un.nt * (BN / 2) + row - BN / 2);
+        else
+          wrow = (size_t)un.e * H + un.nt * BN + row;
+        asrc[j] = (KIND == 0 ? a.gate_up : a.down) + wrow * Kdim + c * 8;
+      }
+#pragma unroll
+      for (int j = 0; j < B_PER; ++j) {
+        const int row = lw * (BM / kWsLoaders) + j * 8 + lane / 8;
+        const int c = (lane % 8) ^ ((row >> 1) & 7);
+        const int rr = row < un.rows ? row : 0;
+        const size_t off = KIND == 0 ? (size_t)a.row_token[un.row0 + rr] * H
+                                     : (size_t)(un.row0 + rr) * I;
+        bsrc[j] = (KIND == 0 ? a.x : a.act) + off + c * 8;
+      }
+    };
+    auto issue = [&](int st) {
+      const int i = st / KT, kt = st - (st / KT) * KT;
+      if (i != cur) {
+        setup(i);
+        cur = i;
+      }
+      uint8_t *buf = smem + (st % kWsStages) * C::STAGE_BYTES;
+#pragma unroll
+      for (int j = 0; j < A_PER; ++j)
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(asrc[j] + kt * BK),
+            (__attribute__((address_space(3))) void *)(buf + (lw * (BN / kWsLoaders) + j * 8) * 128),
+            16, 0, 0);
+#pragma unroll
+      for (int j = 0; j < B_PER; ++j)
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(bsrc[j] + kt * BK),
+            (__attribute__((address_space(3))) void *)(buf + C::A_BYTES +
+                                                       (lw * (BM / kWsLoaders) + j * 8) * 128),
+            16, 0, 0);
+    };
+    for (int st = 0; st < kWsStages - 1 && st < nstages; ++st) issue(st);
+    for (int st = 0; st < nstages; ++st) {
+      // Stage st has landed once at most the loads issued after it remain.
+      const int later = min(kWsStages - 2, nstages - 1 - st);
+      if (later >= 2) wait_vmcnt<2 * PER>();
+      else if (later == 1) wait_vmcnt<PER>();
+      else wait_vmcnt<0>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // Buffer (st - 1) % stages was last read before this barrier.
+      if (st + kWsStages - 1 < nstages) issue(st + kWsStages - 1);
+    }
+    return;
+  }
+
+  // ---- MFMA waves: (wn, wm) = 64 weight rows x 32 tokens, as tile_kernel ----
+  const int wn = wave & 3, wm = wave >> 2;
+  auto a_row = [&](int i) {
+    if (KIND == 0) {
+      constexpr int HALF_T = WNT / 2;
+      return (i < HALF_T ? 0 : BN / 2) + wn * HALF_T * 16 + (i % HALF_T) * 16;
+    }
+    return wn * WNT * 16 + i * 16;
+  };
+  int st = 0;
+  for (int i = 0; i < nu; ++i) {
+    const Unit un = unit_of(i);
+    f32x4 acc[WNT][2];
+#pragma unroll
+    for (int q = 0; q < WNT; ++q) acc[q][0] = acc[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < KT; ++kt, ++st) {
+      lds_barrier();  // stage st published; every read of stage st - 1 is done
+      const uint8_t *abuf = smem + (st % kWsStages) * C::STAGE_BYTES;
+      const uint8_t *bbuf = abuf + C::A_BYTES;
+      const int r = lane & 15, g = lane >> 4;
+      // Every fragment of the stage is requested before the first MFMA, so
+      // the stage costs one LDS round trip.
+      u32x4 bf[KS][2], af[KS][WNT];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int c = 4 * ks + g;
+        bf[ks][0] = *(const u32x4 *)(bbuf + swz<BK>(wm * 32 + r, c));
+        bf[ks][1] = *(const u32x4 *)(bbuf + swz<BK>(wm * 32 + 16 + r, c));
+#pragma unroll
+        for (int q = 0; q < WNT; ++q) af[ks][q] = *(const u32x4 *)(abuf + swz<BK>(a_row(q) + r, c));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int q = 0; q < WNT; ++q) {
+          acc[q][0] = mfma16(af[ks][q], bf[ks][0], acc[q][0]);
+          acc[q][1] = mfma16(af[ks][q], bf[ks][1], acc[q][1]);
+        }
+    }
+    // Epilogue (registers only, no LDS): as tile_kernel.
+    const int g = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int tok = wm * 32 + mt * 16 + (lane & 15);
+      if (KIND == 0) {
+        constexpr int HALF_T = WNT / 2;
+#pragma unroll
+        for (int q = 0; q < HALF_T; ++q) {
+          const f32x4 sg = acc[q][mt], su = acc[q + HALF_T][mt];
+          float v[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float gt = bf16_round(sg[k]);
+            const float up = bf16_round(su[k]);
+            v[k] = gt / (1.0f + expf(-gt)) * up;
+          }
+          u32x2 packed;
+          packed[0] = pack_bf16x2(v[0], v[1]);
+          packed[1] = pack_bf16x2(v[2], v[3]);
+          const int col = un.nt * (BN / 2) + wn * HALF_T * 16 + q * 16 + 4 * g;
+          if (tok < un.rows) *(u32x2 *)(a.act + (size_t)(un.row0 + tok) * I + col) = packed;
+        }
+      } else {
+        const int q0 = tok < un.rows ? a.row_route[un.row0 + tok] : 0;
+#pragma unroll
+        for (int q = 0; q < WNT; ++q) {
+          u32x2 packed;
+          packed[0] = pack_bf16x2(acc[q][mt][0], acc[q][mt][1]);
+          packed[1] = pack_bf16x2(acc[q][mt][2], acc[q][mt][3]);
+          const int col = un.nt * BN + wn * WNT * 16 + q * 16 + 4 * g;
+          if (tok < un.rows) *(u32x2 *)(a.routed + (size_t)q0 * H + col) = packed;
+        }
+      }
+    }
+  }
+}
+
+template <int KIND>
+hipError_t launch_tile_ws(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
+  using C = TileCfg<KIND>;
+  auto k = tile_ws_kernel<KIND>;
+  const size_t lds = (size_t)kWsStages * C::STAGE_BYTES;
+  static bool attr = [&] {
+    return hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)lds) == hipSuccess;
+  }();
+  if (!attr) return hipErrorInvalidValue;
+  int grid = num_cus;
+  if (grid > units_bound) grid = units_bound;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kWsThreads), lds, s, a);
+  return hipGetLastError();
+}
+
+constexpr bool kTileWarpSpecialized = true;
+
 template <int KIND>
 hipError_t launch_tile_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
   using C = TileCfg<KIND>;
@@ -270,10 +501,12 @@ bool tile_shape_ok(int H, int I, bool w4) {
 }
 
 hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
+  if (kTileWarpSpecialized) return launch_tile_ws<0>(a, task_capacity * (a.I / 128), num_cus, s);
   return launch_tile_one<0>(a, task_capacity * (a.I / 128), num_cus, s);
 }
 
 hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
+  if (kTileWarpSpecialized) return launch_tile_ws<1>(a, task_capacity * (a.H / 256), num_cus, s);
   return launch_tile_one<1>(a, task_capacity * (a.H / 256), num_cus, s);
 }
 
