@@ -111,8 +111,8 @@ moe_layout compute_layout(const moe_desc *d) {
   L.offsets = take((size_t)d->E * 4);
   L.ranks = take(R * 4);
   L.map = take(R * 4);
-  L.row_route = take(R * 4 + 32 * 4);  // slack: 32-row scalar reads past R
-  L.row_token = take(R * 4 + 32 * 4);
+  L.row_route = take(R * 4 + 64 * 4);  // slack: scalar reads of up to 64 rows past R
+  L.row_token = take(R * 4 + 64 * 4);
   L.tasks = take(cap * 16);
   L.num_tasks = take(4);
   L.counters = take(2 * 4);

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
 
   // Unit metadata: scalars, plus one VGPR whose lane k < ROWS holds the
   // token (gate/up) or route (down) of the task's row k (one vector load; the
-  // index arrays carry 32 ints of slack past the last row).
+  // index arrays carry 64 ints of slack past the last row).
   const int32_t *row_vec = KIND == 0 ? a.row_token : a.row_route;
   struct Meta {
     int unit, cb, expert, row0, rows;

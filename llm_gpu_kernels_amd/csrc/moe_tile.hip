@@ -325,13 +325,30 @@ __global__ __launch_bounds__(kWsThreads) void tile_ws_kernel(ExpertArgs a) {
           wrow = (size_t)un.e * H + un.nt * BN + row;
         asrc[j] = (KIND == 0 ? a.gate_up : a.down) + wrow * Kdim + c * 8;
       }
+      // Token of each B row through scalar loads (the loaders' vector-memory
+      // counter then holds only their LDS loads, so nothing here waits on
+      // them); rows past the task's end take the task's first token.
+      constexpr int BR = BM / kWsLoaders;  // B rows of this loader wave
+      int tokv[BR];
+      if (KIND == 0) {
+        const MOE_CONST int32_t *rt = as_const(a.row_token) + un.row0;
+        const int t0 = rt[0];
+#pragma unroll
+        for (int k = 0; k < BR; ++k) tokv[k] = lw * BR + k < un.rows ? rt[lw * BR + k] : t0;
+      }
 #pragma unroll
       for (int j = 0; j < B_PER; ++j) {
-        const int row = lw * (BM / kWsLoaders) + j * 8 + lane / 8;
+        const int row = lw * BR + j * 8 + lane / 8;
         const int c = (lane % 8) ^ ((row >> 1) & 7);
-        const int rr = row < un.rows ? row : 0;
-        const size_t off = KIND == 0 ? (size_t)a.row_token[un.row0 + rr] * H
-                                     : (size_t)(un.row0 + rr) * I;
+        size_t off;
+        if (KIND == 0) {
+          int tok = tokv[j * 8];
+#pragma unroll
+          for (int k = 1; k < 8; ++k) tok = lane / 8 == k ? tokv[j * 8 + k] : tok;
+          off = (size_t)tok * H;
+        } else {
+          off = (size_t)(un.row0 + (row < un.rows ? row : 0)) * I;
+        }
         bsrc[j] = (KIND == 0 ? a.x : a.act) + off + c * 8;
       }
     };

@@ -24,7 +24,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native as N
-from .weight_quant import PackedGateUp, TiledGateUp, tile_gate_up
+from .weight_quant import PackedGateUp, RepackedGateUp, TiledGateUp, tile_gate_up
 
 __all__ = [
     "GemmConfig", "FrozenMoEPolicy", "PreparedMoE", "PreparedRoutedMoE", "prepare_moe",
@@ -241,9 +241,9 @@ def prepare_cuda_moe(x, gate_up, down, ids, routing_weights, variant="mfma", dow
 def _as_tiled(packed, device):
     if isinstance(packed, TiledGateUp):
         return packed.to(device)
-    if isinstance(packed, PackedGateUp):
+    if isinstance(packed, (PackedGateUp, RepackedGateUp)):
         return tile_gate_up(packed).to(device)
-    raise TypeError("PackedGateUp or TiledGateUp required")
+    raise TypeError("PackedGateUp, RepackedGateUp or TiledGateUp required")
 
 
 def prepare_w4_moe(x, packed, down, ids, routing_weights, *, down_config=None):
@@ -261,8 +261,9 @@ def prepare_w4_moe(x, packed, down, ids, routing_weights, *, down_config=None):
 
 
 def prepare_w4_layout_moe(x, packed, down, ids, routing_weights, *, down_config=None):
-    """Physical-layout W4 entry (moe_w4_layout_cuda.py:152): the tiled layout is
-    the only W4 layout the gfx950 kernels read."""
+    """Physical-layout W4 entry (moe_w4_layout_cuda.py:152): takes the reference's
+    M24 ``RepackedGateUp`` (or v1 / tiled); the tiled layout is the only W4
+    layout the gfx950 kernels read, and M24 words reach it bit-exactly."""
     return prepare_w4_moe(x, packed, down, ids, routing_weights, down_config=down_config)
 
 

@@ -6,6 +6,11 @@ K % 128 == 0; ``tile_gate_up`` rearranges it into the gfx950 streaming
 layout (role of repack_gate_up, moe_weight_layout.py:81-127), and
 ``dequantize_tiled`` expands tiled weights on the GPU with exactly the decode
 the GEMM uses.  Quantisation and tiling run in the C library on the host.
+
+The reference's M24 physical layout (moe_weight_layout.py:14-19, the
+``repack_gate_up`` output) is read and written bit-exactly by
+``restore_v1_layout`` / ``repack_gate_up``; ``tile_gate_up`` accepts either
+layout.
 """
 from __future__ import annotations
 
@@ -59,6 +64,72 @@ class TiledGateUp:
                            self.logical_shape)
 
 
+# M24 layout string and version of the reference (moe_weight_layout.py:14-17).
+M24_LAYOUT = ("words[E,projection,Ntile,K32,word,Nlane];"
+              "scales[E,projection,Ntile,K128,Nlane];Nlane-contiguous")
+M24_LANES = 64
+
+
+@dataclass(frozen=True)
+class RepackedGateUp:
+    """M24 physical layout: words int32 [E, 2, N/128, K/32, 4, 64] and scales
+    bf16 [E, 2, N/128, K/128, 64] (projection = gate/up half of N, Ntile of 64
+    rows, Nlane innermost), metadata format_version 2."""
+    words: torch.Tensor
+    scales: torch.Tensor
+    metadata: dict = field(default_factory=dict)
+
+    @property
+    def shape(self):
+        e, p, nt, k32, w, nl = self.words.shape
+        return (e, p * nt * nl, k32 * w * 8)
+
+    def to(self, device):
+        return RepackedGateUp(self.words.to(device), self.scales.to(device), self.metadata)
+
+
+def repack_gate_up(packed: PackedGateUp) -> RepackedGateUp:
+    """v1 -> M24, a pure permutation of words and scales (moe_weight_layout.py:81-88):
+    v1 word [e, p*(N/2) + t*64 + l, 4*k + w] -> [e, p, t, k, w, l]; v1 scale
+    [e, p*(N/2) + t*64 + l, g] -> [e, p, t, g, l]."""
+    e, n, k = packed.shape
+    if n % (2 * M24_LANES) or k % GROUP:
+        raise ValueError("M24 layout needs N % 128 == 0 and K % 128 == 0")
+    nt = n // (2 * M24_LANES)
+    words = packed.words.reshape(e, 2, nt, M24_LANES, k // 32, 4).permute(0, 1, 2, 4, 5, 3)
+    scales = packed.scales.reshape(e, 2, nt, M24_LANES, k // GROUP).permute(0, 1, 2, 4, 3)
+    words, scales = words.contiguous(), scales.contiguous()
+    meta = dict(format_version=2, layout=M24_LAYOUT, logical_shape=[e, n, k], group_size=GROUP,
+                canonical_v1_metadata=dict(packed.metadata),
+                physical_words_shape=list(words.shape), physical_scales_shape=list(scales.shape),
+                physical_words_sha256=_digest(words), physical_scales_sha256=_digest(scales))
+    return RepackedGateUp(words, scales, meta)
+
+
+def restore_v1_layout(repacked: RepackedGateUp) -> PackedGateUp:
+    """M24 -> v1 with the original bit patterns (inverse permutation of
+    moe_weight_layout.py:85-88).  Metadata, when present, must declare the M24
+    layout (moe_weight_layout.py:134-141); recorded physical digests are checked."""
+    meta = repacked.metadata or {}
+    if meta and (meta.get("format_version") != 2 or meta.get("layout") != M24_LAYOUT
+                 or meta.get("group_size", GROUP) != GROUP):
+        raise ValueError("unsupported M24 physical layout metadata")
+    words, scales = repacked.words, repacked.scales
+    if (words.ndim != 6 or scales.ndim != 5 or words.shape[4] != 4
+            or words.shape[5] != M24_LANES or words.dtype != torch.int32
+            or scales.dtype != torch.bfloat16 or tuple(scales.shape) != (
+                words.shape[0], words.shape[1], words.shape[2], words.shape[3] // 4, M24_LANES)):
+        raise ValueError("M24 words must be int32 [E,2,Nt,K/32,4,64], scales bf16 [E,2,Nt,K/128,64]")
+    for key, t in (("physical_words_sha256", words), ("physical_scales_sha256", scales)):
+        if key in meta and _digest(t) != meta[key]:
+            raise ValueError(f"M24 buffer does not match its recorded {key}")
+    e, p, nt, k32, _, nl = words.shape
+    n, k = p * nt * nl, k32 * 32
+    v1_words = words.permute(0, 1, 2, 5, 3, 4).reshape(e, n, k // 8).contiguous()
+    v1_scales = scales.permute(0, 1, 2, 4, 3).reshape(e, n, k // GROUP).contiguous()
+    return PackedGateUp(v1_words, v1_scales, dict(meta.get("canonical_v1_metadata", {})))
+
+
 def quantize_gate_up(weight: torch.Tensor) -> PackedGateUp:
     """Quantise a finite, contiguous CPU bf16 [E, N, K] weight (K % 128 == 0)."""
     if weight.device.type != "cpu" or weight.dtype != torch.bfloat16:
@@ -80,8 +151,10 @@ def quantize_gate_up(weight: torch.Tensor) -> PackedGateUp:
     return PackedGateUp(words, scales, meta)
 
 
-def tile_gate_up(packed: PackedGateUp) -> TiledGateUp:
-    """Rearrange v1 words/scales (any device) into the gfx950 layout on the host."""
+def tile_gate_up(packed) -> TiledGateUp:
+    """Rearrange v1 (or M24) words/scales (any device) into the gfx950 layout on the host."""
+    if isinstance(packed, RepackedGateUp):
+        packed = restore_v1_layout(packed.to("cpu"))
     words = packed.words.detach().cpu().contiguous()
     scales = packed.scales.detach().cpu().contiguous()
     e, n, k = packed.shape

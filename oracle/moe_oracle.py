@@ -19,6 +19,9 @@ Pinning of each function (what a plausible mistake would fail):
     invariants plus the golden counts/offsets.
   * quantize_w4 / dequantize_w4: closed-form special cases (all-zero group,
     extremal values, half-way ties, nibble order) and round trip.
+  * m24_repack: element positions computed by hand from the reference's
+    LAYOUT string on distinct-valued inputs, the reference's physical shapes
+    for the Qwen logical shape, and bijectivity.
   * gqa_segmented_reference: PyTorch SDPA math backend on concatenated KV.
 """
 from __future__ import annotations
@@ -258,6 +261,19 @@ def dequantize_w4(words, scales):
     nib = (words.to(torch.int64)[..., None] >> shifts) & 15
     q = (nib.reshape(e, n, kw * 8 // W4_GROUP, W4_GROUP) - 8).float()
     return (q * scales.float()[..., None]).reshape(e, n, kw * 8).to(torch.bfloat16)
+
+
+def m24_repack(words, scales):
+    """v1 -> M24 physical layout, the reference's permutation
+    (src/llm_gpu_kernels/moe_weight_layout.py:85-88, LAYOUT at :14-17 with
+    Ntile = 64 rows): words [E, N, K/8] viewed as [E, 2, N/128, 64, K/32, 4]
+    and permuted to [E, 2, N/128, K/32, 4, 64]; scales [E, N, K/128] viewed as
+    [E, 2, N/128, 64, K/128] and permuted to [E, 2, N/128, K/128, 64]."""
+    e, n, kw = words.shape
+    nt = n // 128
+    w = words.reshape(e, 2, nt, 64, kw // 4, 4).permute(0, 1, 2, 4, 5, 3).contiguous()
+    s = scales.reshape(e, 2, nt, 64, scales.shape[2]).permute(0, 1, 2, 4, 3).contiguous()
+    return w, s
 
 
 # --------------------------------------------------------------------------

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 from llm_gpu_kernels_amd import (GemmConfig, dequantize_tiled, prepare_moe, prepare_routed_moe,
+                                 prepare_w4_layout_moe, repack_gate_up,
                                  prepare_w4_moe, quantize_gate_up, tile_gate_up)
 from llm_gpu_kernels_amd.workloads import make_layer
 from oracle import moe_oracle as O
@@ -181,6 +182,19 @@ def test_w4_token_blocks(tokens, gpu_device):
     for bm in (32, 64):
         m = O.error(outs[bm], outs[16].float().cpu())
         assert m["passed"], (bm, m)
+
+
+def test_w4_m24_layout_entry(gpu_device):
+    """prepare_w4_layout_moe on the reference's M24 physical layout
+    (moe_weight_layout.py:81-127) is bitwise the v1 entry's result."""
+    lay = make_layer("qwen", 17, seed=11, device=gpu_device)
+    ids, w = O.route_topk(lay["logits"].cpu(), 8)
+    ids, w = ids.to(gpu_device), w.to(gpu_device)
+    packed = quantize_gate_up(lay["gate_up"].cpu())
+    a = prepare_w4_moe(lay["x"], packed, lay["down"], ids, w).run().clone()
+    b = prepare_w4_layout_moe(lay["x"], repack_gate_up(packed), lay["down"], ids, w).run().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
 def test_status_bits(gpu_device):
