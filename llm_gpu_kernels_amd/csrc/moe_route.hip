@@ -209,7 +209,8 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
     if (LDSR && ids_in_lds) return s_ids[q];
     return (long long)ids[q];
   };
-  // Pass 1: canonical ranks, 1024 routes per round, two barriers per round.
+  // Pass 1 with the routes in global memory: canonical ranks, 1024 routes per
+  // round, two barriers per round.
   auto rank_round = [&](int r, long long idv, float wv) __attribute__((always_inline)) {
     int (*cnt)[kMaxExperts] = sh.wcnt[r & 1];
     int *next = &sh.wcnt[(r + 1) & 1][0][0];
@@ -244,35 +245,70 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
     for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) next[i] = 0;
     __syncthreads();
     const int rank = ok ? cnt[wave][id] + lrank : -1;
-    if (valid) {
-      a.ranks[q] = rank;
-      if (LDSR) {
-        s_rank[q] = rank;
+    if (valid) a.ranks[q] = rank;
+  };
+  // Chunk of routes each wave ranks on its own (LDSR pass 1): a multiple of
+  // 64 so a wave's sub-rounds are whole waves.
+  const int CH = ((a.R + kPlanWaves - 1) / kPlanWaves + kWave - 1) / kWave * kWave;
+  if constexpr (LDSR) {
+    // Pass 1 with the routes on chip: wave w ranks routes [w*CH, (w+1)*CH)
+    // in 64-route sub-rounds against its own per-expert counters, with no
+    // workgroup barrier; one prefix over the waves (below) then turns the
+    // chunk-local ranks into canonical ones: rank[q] = #{q' < q : id[q'] ==
+    // id[q]} = (routes of that expert in earlier chunks) + (earlier in this
+    // chunk).
+    int *cnt = sh.wcnt[0][wave];
+    // Every sub-round's id and weight are requested before the first one.
+    constexpr int kSub = kLdsRoutes / kPlanWaves / kWave;  // CH <= kSub * 64
+    long long pid[kSub];
+    float pw[kSub];
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+      const int q = wave * CH + j * kWave + lane;
+      const bool valid = j * kWave < CH && q < a.R;
+      pid[j] = valid ? id_of(q) : -1;
+      pw[j] = valid ? (ids_in_lds ? s_w[q] : a.weights[q]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+      if (j * kWave >= CH) break;
+      const int q = wave * CH + j * kWave + lane;
+      const bool valid = q < a.R;
+      const long long idv = pid[j];
+      const float wv = pw[j];
+      const bool ok = valid && idv >= 0 && idv < E;
+      if (valid && !ok) flags |= 1u;
+      if (valid && !isfinite(wv)) flags |= 2u;
+      const int id = ok ? (int)idv : 0;
+      uint64_t match = __ballot(ok);
+#pragma unroll
+      for (int bit = 0; bit < 8; ++bit) {
+        const bool set = (id >> bit) & 1;
+        const uint64_t bb = __ballot(ok && set);
+        match &= set ? bb : ~bb;
+      }
+      const int lrank = __popcll(match & lanemask_lt());
+      // Every lane of a group reads the counter before its first lane (the
+      // only writer) updates it: one wave's LDS operations run in order.
+      const int before = ok ? cnt[id] : 0;
+      if (ok && lrank == 0) cnt[id] = before + __popcll(match);
+      if (valid) {
+        s_rank[q] = ok ? before + lrank : -1;
         if (!ids_in_lds) s_ids[q] = ok ? id : -1;
       }
     }
-  };
-  if constexpr (LDSR) {
-    // Every round's id and weight are requested before the first round, so
-    // the rounds do not each wait a memory round trip after their barrier.
-    constexpr int kRounds = kLdsRoutes / kPlanThreads;
-    long long pid[kRounds];
-    float pw[kRounds];
+    __syncthreads();
+    for (int e = tid; e < E; e += kPlanThreads) {
+      int c = 0;
 #pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      const int q = r * kPlanThreads + tid;
-      pid[r] = -1;
-      pw[r] = 0.f;
-      if (q < a.R) {
-        pid[r] = id_of(q);
-        pw[r] = ids_in_lds ? s_w[q] : a.weights[q];
+      for (int w = 0; w < kPlanWaves; ++w) {
+        const int t = sh.wcnt[0][w][e];
+        sh.wcnt[0][w][e] = c;
+        c += t;
       }
+      sh.run[e] = c;
     }
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      if (r * kPlanThreads >= a.R) break;
-      rank_round(r, pid[r], pw[r]);
-    }
+    __syncthreads();
   } else {
     for (int r = 0; r * kPlanThreads < a.R; ++r) {
       const int q = r * kPlanThreads + tid;
@@ -329,6 +365,12 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
     if (LDSR) {
       idv = s_ids[q];
       rank = s_rank[q];
+      if (rank >= 0) {
+        rank += sh.wcnt[0][q / CH][idv];
+        a.ranks[q] = rank;
+      } else {
+        a.ranks[q] = -1;
+      }
     } else {
       idv = (long long)ids[q];
       rank = a.ranks[q];  // written by this thread in pass 1
