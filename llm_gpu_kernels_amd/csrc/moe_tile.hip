@@ -9,10 +9,10 @@
 // same XCD, whose L2 then serves the repeated weight tile.
 //
 // Per unit: a K loop over BK-wide stages.  Each stage's weight tile [BN][BK]
-// and token tile [BM][BK] are loaded global -> registers (two stages in
-// flight) -> LDS, 16-byte chunks XOR-swizzled by row so that the MFMA
-// operand reads are bank-conflict free, then 8 waves (4 along N x 2 along M)
-// run 16x16x32 bf16 MFMAs.  (W4G128 gate/up with many rows per expert runs in
+// and token tile [BM][BK] go global -> LDS (the warp-specialised kernel
+// below), 16-byte chunks XOR-swizzled by row so that the MFMA operand reads
+// are bank-conflict free, then 8 waves (4 along N x 2 along M) run 16x16x32
+// bf16 MFMAs.  (W4G128 gate/up with many rows per expert runs in
 // the wave kernel of moe_wave.hip, which decodes each weight once into MFMA
 // registers; the down weights are bf16 in both formats.)
 //
@@ -27,8 +27,6 @@ namespace moe {
 
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = 8;
 constexpr int BM = 64;
 
 template <typename T>
@@ -62,186 +60,13 @@ struct TileCfg {
   static constexpr int A_BYTES = BN * BK * 2;
   static constexpr int B_BYTES = BM * BK * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int A_LOADS = A_BYTES / 1024 / kWaves;  // 16-B loads per lane
-  static constexpr int B_LOADS = B_BYTES / 1024 / kWaves;
   static constexpr int OUT_COLS = KIND == 0 ? BN / 2 : BN;  // output columns per n-tile
 };
 
-template <int KIND>
-__global__ __launch_bounds__(kThreads) void tile_kernel(ExpertArgs a) {
-  using C = TileCfg<KIND>;
-  constexpr int BN = C::BN, BK = C::BK, WNT = C::WNT;
-  constexpr int KS = BK / 32;  // MFMA k-steps per stage
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wn = wave & 3, wm = wave >> 2;
-  const int H = a.H, I = a.I;
-  const int Kdim = KIND == 0 ? H : I;
-  const int KT = Kdim / BK;  // even, >= 2 (checked on the host)
-  const int ntiles = (KIND == 0 ? I : H) / C::OUT_COLS;
-  const int num_tasks = *as_const(a.num_tasks);
-  const int total = num_tasks * ntiles;
-  const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
-
-  // XCD-aware slot: the first-wave dispatch places workgroup b on XCD b % 8,
-  // so slot numbers run contiguously within an XCD.
-  const int G = gridDim.x;
-  const int slot = (G % 8) ? (int)blockIdx.x : (int)(blockIdx.x / 8 + (blockIdx.x % 8) * (G / 8));
-
-  for (int u = slot; u < total; u += G) {
-    // Units come in blocks of kTaskBlock consecutive tasks (the task list is
-    // expert-major), column-tile-major within a block: a block's tasks share
-    // each weight tile of their expert, and the block's token rows stay in
-    // the one L2 that runs the block for all of its column tiles.
-    const int blk = u / (kTaskBlock * ntiles);
-    const int rem = u - blk * (kTaskBlock * ntiles);
-    const int mb = min(kTaskBlock, num_tasks - blk * kTaskBlock);
-    const int nt = rem / mb;
-    const int t = blk * kTaskBlock + (rem - nt * mb);
-    const int e = tasks[4 * t], row0 = tasks[4 * t + 1], rows = tasks[4 * t + 2];
-
-    // --- per-lane global sources of this unit -------------------------------
-    // Token tile rows: 8 rows per 1 KB load (64-K stages).
-    constexpr int B_RPL = 1024 / (BK * 2);  // rows per 1 KB
-    const uint16_t *bsrc[C::B_LOADS];
-    int brow[C::B_LOADS];
-#pragma unroll
-    for (int i = 0; i < C::B_LOADS; ++i) {
-      const int row = (wave * C::B_LOADS + i) * B_RPL + lane / (BK / 8);
-      brow[i] = row;
-      const int rr = row < rows ? row : 0;
-      size_t off;
-      if (KIND == 0) off = (size_t)a.row_token[row0 + rr] * H;
-      else off = (size_t)(row0 + rr) * I;
-      bsrc[i] = (KIND == 0 ? a.x : a.act) + off + (lane % (BK / 8)) * 8;
-    }
-    const uint16_t *asrc[C::A_LOADS];
-    int arow[C::A_LOADS];
-#pragma unroll
-    for (int i = 0; i < C::A_LOADS; ++i) {
-      const int row = (wave * C::A_LOADS + i) * 8 + lane / 8;  // tile row
-      arow[i] = row;
-      size_t wrow;
-      if (KIND == 0)
-        wrow = (size_t)e * 2 * I + (row < BN / 2 ? nt * (BN / 2) + row : I + nt * (BN / 2) + row - BN / 2);
-      else
-        wrow = (size_t)e * H + nt * BN + row;
-      asrc[i] = (KIND == 0 ? a.gate_up : a.down) + wrow * Kdim + (lane % 8) * 8;
-    }
-
-    // --- register stage sets ---------------------------------------------
-    struct Regs {
-      u32x4 a[C::A_LOADS];
-      u32x4 b[C::B_LOADS];
-    };
-    auto gload = [&](Regs &R, int kt) {
-#pragma unroll
-      for (int i = 0; i < C::A_LOADS; ++i) R.a[i] = *(const u32x4 *)(asrc[i] + kt * BK);
-#pragma unroll
-      for (int i = 0; i < C::B_LOADS; ++i) R.b[i] = *(const u32x4 *)(bsrc[i] + kt * BK);
-    };
-    auto sts = [&](uint8_t *buf, const Regs &R) {
-      uint8_t *abuf = buf, *bbuf = buf + C::A_BYTES;
-#pragma unroll
-      for (int i = 0; i < C::A_LOADS; ++i) *(u32x4 *)(abuf + swz<BK>(arow[i], lane % 8)) = R.a[i];
-#pragma unroll
-      for (int i = 0; i < C::B_LOADS; ++i)
-        *(u32x4 *)(bbuf + swz<BK>(brow[i], lane % (BK / 8))) = R.b[i];
-    };
-
-    // --- MFMA on one LDS stage ------------------------------------------------
-    // Wave (wn, wm): weight row tiles (gate/up: wn's slice of both halves),
-    // token tiles wm*32 + {0, 16}.  Lane l reads row l%16, chunk 4*ks + l/16.
-    f32x4 acc[WNT][2];
-#pragma unroll
-    for (int i = 0; i < WNT; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto a_row = [&](int i) {
-      if (KIND == 0) {
-        constexpr int HALF_T = WNT / 2;  // tiles per half per wave
-        return (i < HALF_T ? 0 : BN / 2) + wn * HALF_T * 16 + (i % HALF_T) * 16;
-      }
-      return wn * WNT * 16 + i * 16;
-    };
-    auto compute = [&](const uint8_t *buf) {
-      const uint8_t *abuf = buf, *bbuf = buf + C::A_BYTES;
-      const int r = lane & 15, g = lane >> 4;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int c = 4 * ks + g;
-        const u32x4 b0 = *(const u32x4 *)(bbuf + swz<BK>(wm * 32 + r, c));
-        const u32x4 b1 = *(const u32x4 *)(bbuf + swz<BK>(wm * 32 + 16 + r, c));
-#pragma unroll
-        for (int i = 0; i < WNT; ++i) {
-          const u32x4 af = *(const u32x4 *)(abuf + swz<BK>(a_row(i) + r, c));
-          acc[i][0] = mfma16(af, b0, acc[i][0]);
-          acc[i][1] = mfma16(af, b1, acc[i][1]);
-        }
-      }
-    };
-
-    uint8_t *buf0 = smem, *buf1 = smem + C::STAGE_BYTES;
-    Regs R0, R1;
-    gload(R0, 0);
-    gload(R1, 1);
-    sts(buf0, R0);
-    gload(R0, 2 < KT ? 2 : KT - 1);
-    lds_barrier();
-    for (int kt = 0; kt < KT; kt += 2) {
-      compute(buf0);
-      sts(buf1, R1);  // stage kt+1
-      gload(R1, kt + 3 < KT ? kt + 3 : KT - 1);
-      lds_barrier();
-      compute(buf1);
-      sts(buf0, R0);  // stage kt+2 (a harmless copy of the last stage at the end)
-      gload(R0, kt + 4 < KT ? kt + 4 : KT - 1);
-      lds_barrier();
-    }
-
-    // --- epilogue: lane holds rows 4*(l/16)+i of its 16-row tile, token l%16 --
-    const int g = lane >> 4;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int tok = wm * 32 + mt * 16 + (lane & 15);
-      if (KIND == 0) {
-        constexpr int HALF_T = WNT / 2;
-#pragma unroll
-        for (int i = 0; i < HALF_T; ++i) {
-          const f32x4 sg = acc[i][mt], su = acc[i + HALF_T][mt];
-          float v[4];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float gt = bf16_round(sg[k]);
-            const float up = bf16_round(su[k]);
-            v[k] = gt / (1.0f + expf(-gt)) * up;
-          }
-          u32x2 packed;
-          packed[0] = pack_bf16x2(v[0], v[1]);
-          packed[1] = pack_bf16x2(v[2], v[3]);
-          const int col = nt * (BN / 2) + wn * HALF_T * 16 + i * 16 + 4 * g;
-          if (tok < rows) *(u32x2 *)(a.act + (size_t)(row0 + tok) * I + col) = packed;
-        }
-      } else {
-        const int q = tok < rows ? a.row_route[row0 + tok] : 0;
-#pragma unroll
-        for (int i = 0; i < WNT; ++i) {
-          u32x2 packed;
-          packed[0] = pack_bf16x2(acc[i][mt][0], acc[i][mt][1]);
-          packed[1] = pack_bf16x2(acc[i][mt][2], acc[i][mt][3]);
-          const int col = nt * BN + wn * WNT * 16 + i * 16 + 4 * g;
-          if (tok < rows) *(u32x2 *)(a.routed + (size_t)q * H + col) = packed;
-        }
-      }
-    }
-    lds_barrier();  // the next unit's prologue rewrites buf0
-  }
-}
-
-// ---- warp-specialised variant ------------------------------------------------
-// The same units, tiles and MFMA work, with the K stages moved by global ->
-// LDS direct loads (16 bytes per lane, gfx950) into a ring of kWsStages LDS
-// stages, kWsStages - 1 stages ahead of the matrix cores.  Four loader waves
+// ---- warp-specialised kernel ---------------------------------------------------
+// The K stages move by global -> LDS direct loads (16 bytes per lane, gfx950)
+// into a ring of kWsStages LDS stages, kWsStages - 1 stages ahead of the
+// matrix cores.  Four loader waves
 // issue every load and carry every vector-memory wait; the eight MFMA waves
 // only read LDS.  One workgroup barrier per stage publishes that stage (the
 // loaders waited for it) and frees the oldest buffer (every MFMA wave has
@@ -282,7 +107,7 @@ __global__ __launch_bounds__(kWsThreads) void tile_ws_kernel(ExpertArgs a) {
   const int nu = slot < total ? (total - slot + G - 1) / G : 0;
   const int nstages = nu * KT;
 
-  // Unit i of this workgroup (same order and task blocks as tile_kernel).
+  // Unit i of this workgroup: blocks of kTaskBlock tasks, n-tile-major within a block.
   struct Unit {
     int e, row0, rows, nt;
   };
@@ -389,7 +214,7 @@ __global__ __launch_bounds__(kWsThreads) void tile_ws_kernel(ExpertArgs a) {
     return;
   }
 
-  // ---- MFMA waves: (wn, wm) = 64 weight rows x 32 tokens, as tile_kernel ----
+  // ---- MFMA waves: (wn, wm) = 64 weight rows x 32 tokens ------------------
   const int wn = wave & 3, wm = wave >> 2;
   auto a_row = [&](int i) {
     if (KIND == 0) {
@@ -429,7 +254,8 @@ __global__ __launch_bounds__(kWsThreads) void tile_ws_kernel(ExpertArgs a) {
           acc[q][1] = mfma16(af[ks][q], bf[ks][1], acc[q][1]);
         }
     }
-    // Epilogue (registers only, no LDS): as tile_kernel.
+    // Epilogue (registers only, no LDS): lane holds rows 4*(l/16)+k of its
+    // 16-row weight tile for token l%16.
     const int g = lane >> 4;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -484,29 +310,6 @@ hipError_t launch_tile_ws(const ExpertArgs &a, int units_bound, int num_cus, hip
   return hipGetLastError();
 }
 
-constexpr bool kTileWarpSpecialized = true;
-
-template <int KIND>
-hipError_t launch_tile_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
-  using C = TileCfg<KIND>;
-  auto k = tile_kernel<KIND>;
-  const size_t lds = 2 * (size_t)C::STAGE_BYTES;
-  static int per_cu = [&] {
-    int n = 1;
-    (void)hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)kMaxLds);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k, kThreads, lds) !=
-            hipSuccess || n < 1)
-      n = 1;
-    return n;
-  }();
-  int grid = num_cus * per_cu;
-  if (grid > units_bound) grid = units_bound;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, s, a);
-  return hipGetLastError();
-}
-
 }  // namespace
 
 bool tile_shape_ok(int H, int I, bool w4) {
@@ -518,13 +321,11 @@ bool tile_shape_ok(int H, int I, bool w4) {
 }
 
 hipError_t launch_tile_gate_up(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
-  if (kTileWarpSpecialized) return launch_tile_ws<0>(a, task_capacity * (a.I / 128), num_cus, s);
-  return launch_tile_one<0>(a, task_capacity * (a.I / 128), num_cus, s);
+  return launch_tile_ws<0>(a, task_capacity * (a.I / 128), num_cus, s);
 }
 
 hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus, hipStream_t s) {
-  if (kTileWarpSpecialized) return launch_tile_ws<1>(a, task_capacity * (a.H / 256), num_cus, s);
-  return launch_tile_one<1>(a, task_capacity * (a.H / 256), num_cus, s);
+  return launch_tile_ws<1>(a, task_capacity * (a.H / 256), num_cus, s);
 }
 
 }  // namespace moe
