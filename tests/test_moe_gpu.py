@@ -197,6 +197,51 @@ def test_w4_m24_layout_entry(gpu_device):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize("tokens", [1, 2, 5, 33])
+@pytest.mark.parametrize("w4", [False, True])
+def test_streaming_unit_blocks(tokens, w4, gpu_device):
+    """Qwen shape at small T: fewer units than workgroups (T=1), a unit block
+    per workgroup spanning several tasks (T=33), every expert receiving one
+    route or many; the streaming kernels' unit blocks against the oracle."""
+    lay = make_layer("qwen", tokens, seed=40 + tokens, device=gpu_device)
+    ids, w = O.route_topk(lay["logits"].cpu(), 8)
+    ids, w = ids.to(gpu_device), w.to(gpu_device)
+    if w4:
+        packed = quantize_gate_up(lay["gate_up"].cpu())
+        plan = prepare_w4_moe(lay["x"], packed, lay["down"], ids, w)
+        ref_gu = O.dequantize_w4(packed.words, packed.scales)
+    else:
+        plan = prepare_moe(lay["x"], lay["gate_up"], lay["down"], ids, w)
+        ref_gu = lay["gate_up"].cpu()
+    assert plan.layout.fast_path == 1
+    out = plan.run().clone()
+    torch.cuda.synchronize()
+    ref = O.moe_reference(lay["x"].cpu(), ref_gu, lay["down"].cpu(), ids.cpu(), w.cpu())
+    m = O.error(out, ref)
+    assert m["passed"], m
+
+
+def test_streaming_one_hot_expert(gpu_device):
+    """Every route of every token on expert 5 (one task of 16 rows per 16
+    routes, all units of the launch on one expert), then a re-run with spread
+    routes on the same prepared object."""
+    lay = make_layer("qwen", 4, seed=77, device=gpu_device)
+    ids = torch.full((4, 8), 5, dtype=torch.int32, device=gpu_device)
+    w = torch.full((4, 8), 0.125, dtype=torch.float32, device=gpu_device)
+    plan = prepare_moe(lay["x"], lay["gate_up"], lay["down"], ids, w)
+    out = plan.run().clone()
+    torch.cuda.synchronize()
+    ref = O.moe_reference(lay["x"].cpu(), lay["gate_up"].cpu(), lay["down"].cpu(), ids.cpu(), w.cpu())
+    assert O.error(out, ref)["passed"]
+    ni, nw = O.route_topk(lay["logits"].cpu(), 8)
+    ids.copy_(ni.to(gpu_device))
+    w.copy_(nw.to(gpu_device))
+    out = plan.run().clone()
+    torch.cuda.synchronize()
+    ref = O.moe_reference(lay["x"].cpu(), lay["gate_up"].cpu(), lay["down"].cpu(), ni, nw)
+    assert O.error(out, ref)["passed"]
+
+
 def test_status_bits(gpu_device):
     x, gu, dn, ids, rw = O.make_inputs(tokens=3, experts=4, topk=2, hidden=128, intermediate=128,
                                        id_dtype=torch.int32, pattern="random", seed=101)
