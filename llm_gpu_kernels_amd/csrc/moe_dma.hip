@@ -1,0 +1,338 @@
+// bf16 weight-streaming grouped GEMMs with global -> LDS direct loads, for
+// few rows per expert (the streaming regime of moe_stream.hip): gate/up +
+// SwiGLU (reference: _dynamic_grouped_gate_up_swiglu, moe_fused.py:18-73;
+// cuda_gate_up_bf16, cuda_gate_up.cu:53-131) and the down projection
+// (_dynamic_grouped, moe.py:69-95).
+//
+// Same units as the register-streaming kernel -- (task, 16 act columns) with
+// 16 gate + 16 up weight rows, or (task, 32 hidden columns) -- and the same
+// split-K over eight MFMA waves with a fixed-order reduction, but the weights
+// reach the matrix cores through LDS:
+//  * four loader waves move each unit's 32 weight rows in K-stages of KC
+//    elements with gfx950's 16-byte global -> LDS loads; every load
+//    instruction reads one contiguous 1 KiB piece (one row's KC = 512
+//    elements, or two rows' 256), the pattern HBM streams fastest (6.5 TB/s
+//    measured, against 5.3-5.6 TB/s for the 16 rows x 64 bytes of a direct
+//    MFMA-operand load).  The loaders own every wait on those loads;
+//  * the stages form a ring of NS buffers in LDS, NS - 1 stages ahead; one
+//    workgroup barrier per stage publishes a stage and frees the oldest;
+//  * the MFMA waves read their K-slice of a stage as MFMA A fragments
+//    (16-byte chunks XOR-swizzled by row on the global side, so the reads are
+//    bank-conflict free) against token rows held in registers for the whole
+//    task (reloaded only on a task switch, on the MFMA waves' own counter);
+//  * a unit's eight partial tiles are written to LDS after its last stage and
+//    reduced, in fixed wave order, after the next stage barrier.
+// One 768-thread workgroup per CU; persistent workgroups take blocks of
+// consecutive units.  Rounding as in moe_stream.hip.
+#include "common.h"
+#include "moe_internal.h"
+
+#define MOE_CONST __attribute__((address_space(4)))
+
+namespace moe {
+
+namespace {
+
+constexpr int kConsumers = 8;
+constexpr int kLoaders = 4;
+constexpr int kThreads = (kConsumers + kLoaders) * kWave;
+constexpr int kRows = 32;  // weight rows per unit
+constexpr int kWaitVmcntZero = (7 << 4) | (15 << 8);
+
+template <typename T>
+__device__ __forceinline__ const MOE_CONST T *as_const(const T *p) {
+  return (const MOE_CONST T *)p;
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Loader barrier: no fence (a release fence would wait for the loader's own
+// LDS loads, which is exactly what the ring must not do); compiler barriers
+// keep the loads on their side of it.
+__device__ __forceinline__ void loader_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int KIND, int MT>
+struct DmaCfg {
+  static constexpr int KC = KIND == 0 ? 512 : 256;      // K per stage
+  static constexpr int STAGE = kRows * KC * 2;            // bytes
+  static constexpr int KKS = KC / kConsumers / 32;        // k-steps per wave per stage
+  static constexpr int RED = 2 * kConsumers * 2 * MT * kWave * 16;  // partials, 2 parities
+  static constexpr int NS0 = (int)((kMaxLds - RED) / STAGE);
+  static constexpr int NS = NS0 > 8 ? 8 : NS0;
+  static constexpr int PER = STAGE / 1024 / kLoaders;     // 1 KiB loads per stage per loader
+  static_assert(NS >= 3, "at least two stages ahead");
+  static_assert((NS - 2) * PER < 64, "vmcnt range");
+};
+
+// Byte offset in a stage of 16-byte chunk c of stage row R (rows of KC elements).
+template <int KC>
+__device__ __forceinline__ int stage_off(int R, int c) {
+  return R * (KC * 2) + ((c ^ (R & 15)) << 4);
+}
+
+template <int KIND, int MT, int SPU>
+__global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
+  using C = DmaCfg<KIND, MT>;
+  constexpr int KC = C::KC, KKS = C::KKS, NS = C::NS, PER = C::PER;
+  constexpr int NRB = 2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  f32x4 *s_red = (f32x4 *)(smem + NS * C::STAGE);  // [2][kConsumers][NRB][MT][64]
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & (kWave - 1);
+  const int H = a.H, I = a.I;
+  const int K = KIND == 0 ? H : I;  // == SPU * KC (checked on the host)
+  const int ncb = KIND == 0 ? I / 16 : H / 32;  // units per task
+  const int total = *as_const(a.num_tasks) * ncb;
+  const int G = gridDim.x;
+  const int cper = (total + G - 1) / G;
+  const int b0 = (int)blockIdx.x * cper;
+  const int count = b0 < total ? min(cper, total - b0) : 0;
+  if (count <= 0) return;
+  const int nstages = count * SPU;
+  const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
+
+  if (wave >= kConsumers) {
+    // ---- loaders ------------------------------------------------------------
+    const int lw = wave - kConsumers;
+    // Load j of this wave covers stage rows R0 .. R0 + RPI - 1, RPI = 1024 / (2 KC)
+    // rows per 1 KiB; lane l writes LDS byte 16 l of the piece.
+    constexpr int RPI = 1024 / (KC * 2);
+    constexpr int LPR = kWave / RPI;  // lanes per row
+    const int lrow = lane / LPR, lch = lane % LPR;
+    int cur = -1;
+    const uint16_t *src[PER];
+    auto setup = [&](int u) {
+      const int t = u / ncb, cb = u - t * ncb;
+      const int e = tasks[4 * t];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int R = (lw * PER + j) * RPI + lrow;  // stage row
+        size_t grow;
+        if (KIND == 0) grow = (size_t)e * 2 * I + (R < 16 ? cb * 16 + R : I + cb * 16 + R - 16);
+        else grow = (size_t)e * H + cb * 32 + R;
+        const int c = lch ^ (R & 15);  // the chunk that belongs at LDS chunk lch
+        src[j] = (KIND == 0 ? a.gate_up : a.down) + grow * K + c * 8;
+      }
+    };
+    auto issue = [&](int st) {
+      const int i = st / SPU, s = st - (st / SPU) * SPU;
+      if (i != cur) {
+        setup(b0 + i);
+        cur = i;
+      }
+      uint8_t *buf = smem + (st % NS) * C::STAGE;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        __builtin_amdgcn_global_load_lds(
+            (const void *)(src[j] + s * KC),
+            (__attribute__((address_space(3))) void *)(buf + (lw * PER + j) * 1024), 16, 0, 0);
+    };
+    for (int st = 0; st < NS - 1 && st < nstages; ++st) issue(st);
+    for (int st = 0; st < nstages; ++st) {
+      // Stage st has landed once at most the loads issued after it remain.
+      const int later = min(NS - 2, nstages - 1 - st);
+      switch (later) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<PER>(); break;
+        case 2: wait_vmcnt<(NS > 3 ? 2 : 0) * PER>(); break;
+        case 3: wait_vmcnt<(NS > 4 ? 3 : 0) * PER>(); break;
+        case 4: wait_vmcnt<(NS > 5 ? 4 : 0) * PER>(); break;
+        case 5: wait_vmcnt<(NS > 6 ? 5 : 0) * PER>(); break;
+        default: wait_vmcnt<(NS > 7 ? 6 : 0) * PER>(); break;
+      }
+      loader_barrier();
+      // Buffer (st - 1) % NS was last read before this barrier.
+      if (st + NS - 1 < nstages) issue(st + NS - 1);
+    }
+    loader_barrier();  // the MFMA waves' last reduction barrier
+    return;
+  }
+
+  // ---- MFMA waves: wave w owns K-slice [w * KC / 8, +KC / 8) of every stage --
+  const int r = lane & 15, g = lane >> 4;
+  struct Meta {
+    int task, cb, row0, rows;
+    int idxv;  // lane k < 32: token (gate/up) or route (down) of row k
+  };
+  const int32_t *row_vec = KIND == 0 ? a.row_token : a.row_route;
+  auto meta_of = [&](int u) {
+    Meta m;
+    m.task = u / ncb;
+    m.cb = u - m.task * ncb;
+    m.row0 = tasks[4 * m.task + 1];
+    m.rows = tasks[4 * m.task + 2];
+    m.idxv = row_vec[m.row0 + (lane & 31)];
+    return m;
+  };
+
+  // Token rows of the task: fragment [mt][s * KKS + kk] = row mt*16 + r,
+  // K = s*KC + wave*KC/8 + kk*32 + 8g .. +8.  Rows past the task's end read
+  // row 0 (finite data in columns the epilogue never stores).
+  u32x4 bfr[MT][SPU * KKS];
+  auto load_b = [&](const Meta &m) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int j = mt * 16 + r;
+      const bool ok = j < m.rows;
+      size_t row;
+      if (KIND == 0) row = (size_t)(ok ? __shfl(m.idxv, j, kWave) : 0) * H;
+      else row = (size_t)(ok ? m.row0 + j : 0) * I;
+      const uint16_t *b = (KIND == 0 ? a.x : a.act) + row + wave * (KC / 8) + g * 8;
+#pragma unroll
+      for (int s = 0; s < SPU; ++s)
+#pragma unroll
+        for (int kk = 0; kk < KKS; ++kk) bfr[mt][s * KKS + kk] = *(const u32x4 *)(b + s * KC + kk * 32);
+    }
+  };
+
+  auto epilogue = [&](const Meta &m, int parity) {
+    const f32x4 *red = s_red + (size_t)parity * kConsumers * NRB * MT * kWave;
+    if (KIND == 0) {
+      if (tid < MT * 4 * kWave) {
+        const int l = tid & 63, i = (tid >> 6) & 3, mt = tid >> 8;
+        const int j = mt * 16 + (l & 15);
+        const float *redf = (const float *)red;
+        auto part = [&](int w, int rb) { return redf[(((w * NRB + rb) * MT + mt) * kWave + l) * 4 + i]; };
+        float sg = part(0, 0), su = part(0, 1);
+#pragma unroll
+        for (int w = 1; w < kConsumers; ++w) {
+          sg += part(w, 0);
+          su += part(w, 1);
+        }
+        const float gt = bf16_round(sg);
+        const float up = bf16_round(su);
+        const float v = gt / (1.0f + expf(-gt)) * up;
+        if (j < m.rows)
+          a.act[(size_t)(m.row0 + j) * I + m.cb * 16 + 4 * (l >> 4) + i] =
+              (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+      }
+    } else {
+      if (tid < NRB * MT * kWave) {
+        const int rb = tid / (MT * kWave);
+        const int mt = (tid >> 6) % MT, l = tid & 63;
+        const int j = mt * 16 + (l & 15);
+        f32x4 sm = red[(rb * MT + mt) * kWave + l];
+#pragma unroll
+        for (int w = 1; w < kConsumers; ++w) sm += red[((w * NRB + rb) * MT + mt) * kWave + l];
+        const int q = __shfl(m.idxv, j, kWave);
+        u32x2 packed;
+        packed[0] = pack_bf16x2(sm[0], sm[1]);
+        packed[1] = pack_bf16x2(sm[2], sm[3]);
+        if (j < m.rows)
+          *(u32x2 *)(a.routed + (size_t)q * H + m.cb * 32 + rb * 16 + 4 * (l >> 4)) = packed;
+      }
+    }
+  };
+
+  Meta prev;
+  prev.task = -1;
+  int btask = -1;
+  int st = 0;
+  for (int i = 0; i < count; ++i) {
+    const Meta cur = meta_of(b0 + i);
+    if (cur.task != btask) {
+      load_b(cur);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+      btask = cur.task;
+    }
+    f32x4 acc[NRB][MT];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < SPU; ++s, ++st) {
+      lds_barrier();  // stage st published; unit i-1's partials published
+      if (s == 0 && i > 0) epilogue(prev, (i - 1) & 1);
+      const uint8_t *buf = smem + (st % NS) * C::STAGE;
+      u32x4 af[KKS][NRB];
+#pragma unroll
+      for (int kk = 0; kk < KKS; ++kk)
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+          const int c = wave * (KC / 64) + kk * 4 + g;
+          af[kk][rb] = *(const u32x4 *)(buf + stage_off<KC>(rb * 16 + r, c));
+        }
+#pragma unroll
+      for (int kk = 0; kk < KKS; ++kk)
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[rb][mt] = mfma16(af[kk][rb], bfr[mt][s * KKS + kk], acc[rb][mt]);
+    }
+    // Partials of unit i (parity i & 1), reduced after the next barrier.
+    f32x4 *red = s_red + (size_t)(i & 1) * kConsumers * NRB * MT * kWave;
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((wave * NRB + rb) * MT + mt) * kWave + lane] = acc[rb][mt];
+    prev = cur;
+  }
+  lds_barrier();
+  epilogue(prev, (count - 1) & 1);
+}
+
+template <int KIND, int MT, int SPU>
+hipError_t launch_one(const ExpertArgs &a, int num_cus, hipStream_t s) {
+  using C = DmaCfg<KIND, MT>;
+  auto k = dma_kernel<KIND, MT, SPU>;
+  const size_t lds = (size_t)C::NS * C::STAGE + C::RED;
+  static const bool attr = hipFuncSetAttribute((const void *)k,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lds) == hipSuccess;
+  if (!attr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(num_cus > 0 ? num_cus : 1), dim3(kThreads), lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// gate/up: K = H in 2 or 4 stages of 512 (8 with 16-row tasks); down: K = I
+// in 2, 3 or 4 stages of 256.
+bool dma_shape_ok(int H, int I, int token_block) {
+  return (H == 1024 || H == 2048 || (H == 4096 && token_block == 16)) &&
+         (I == 512 || I == 768 || I == 1024);
+}
+
+namespace {
+template <int KIND, int MT>
+hipError_t launch_spu(const ExpertArgs &a, int spu, int num_cus, hipStream_t s) {
+  if (spu == 2) return launch_one<KIND, MT, 2>(a, num_cus, s);
+  if (spu == 4) return launch_one<KIND, MT, 4>(a, num_cus, s);
+  if constexpr (KIND == 1) {
+    if (spu == 3) return launch_one<KIND, MT, 3>(a, num_cus, s);
+  } else if constexpr (MT == 1) {
+    if (spu == 8) return launch_one<KIND, MT, 8>(a, num_cus, s);
+  }
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+hipError_t launch_dma_gate_up(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s) {
+  const int spu = a.H / 512;
+  return token_block == 16 ? launch_spu<0, 1>(a, spu, num_cus, s) : launch_spu<0, 2>(a, spu, num_cus, s);
+}
+
+hipError_t launch_dma_down(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s) {
+  const int spu = a.I / 256;
+  return token_block == 16 ? launch_spu<1, 1>(a, spu, num_cus, s) : launch_spu<1, 2>(a, spu, num_cus, s);
+}
+
+}  // namespace moe

@@ -138,6 +138,11 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(const uint32_t *__restr
   for (int j = 0; j < 4; ++j) *(u32x4 *)(row + 32 * j) = w4_decode8(w[j], ks);
 }
 
+// bf16 streaming GEMMs through LDS (moe_dma.hip) rather than straight into
+// registers (moe_stream.hip), where the shape allows.
+constexpr bool kDmaStreaming = true;
+constexpr bool kDmaDown = true;
+
 }  // namespace
 
 hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
@@ -149,7 +154,11 @@ hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_bloc
       wave_w4_shape_ok(a.H, a.I, token_block))
     return launch_wave_w4_gate_up(a, task_capacity, token_block, s);
   if (path == kTile) return w4 ? hipErrorInvalidValue : launch_tile_gate_up(a, task_capacity, num_cus, s);
-  if (path == kStream) return launch_stream_gate_up(a, task_capacity, token_block, w4, num_cus, s);
+  if (path == kStream) {
+    if (!w4 && kDmaStreaming && dma_shape_ok(a.H, a.I, token_block))
+      return launch_dma_gate_up(a, token_block, num_cus, s);
+    return launch_stream_gate_up(a, task_capacity, token_block, w4, num_cus, s);
+  }
   if (w4) return hipErrorInvalidValue;
   const dim3 grid(task_capacity, (token_block * a.I + 255) / 256);
   hipLaunchKernelGGL(gate_up_generic_kernel, grid, dim3(256), 0, s, a, token_block);
@@ -159,7 +168,10 @@ hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_bloc
 hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, int path,
                        int num_cus, hipStream_t s) {
   if (path == kTile) return launch_tile_down(a, task_capacity, num_cus, s);
-  if (path == kStream) return launch_stream_down(a, task_capacity, token_block, num_cus, s);
+  if (path == kStream) {
+    if (kDmaStreaming && kDmaDown && dma_shape_ok(a.H, a.I, token_block)) return launch_dma_down(a, token_block, num_cus, s);
+    return launch_stream_down(a, task_capacity, token_block, num_cus, s);
+  }
   const dim3 grid(task_capacity, (token_block * a.H + 255) / 256);
   hipLaunchKernelGGL(down_generic_kernel, grid, dim3(256), 0, s, a, token_block);
   return hipGetLastError();

@@ -55,6 +55,10 @@ hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int tok
 hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,
                               int num_cus, hipStream_t s);
 bool stream_shape_ok(int H, int I, bool w4);
+// bf16 streaming GEMMs through LDS (16/32-row tasks), moe_dma.hip.
+bool dma_shape_ok(int H, int I, int token_block);
+hipError_t launch_dma_gate_up(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s);
+hipError_t launch_dma_down(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s);
 // W4 gate/up + SwiGLU, one unit per wave with K-chunked token rows in LDS, for
 // tasks with several rows per expert (token_block 16, 32 or 64).
 bool wave_w4_shape_ok(int H, int I, int token_block);
