@@ -8,7 +8,7 @@
 // 16 gate + 16 up weight rows, or (task, 32 hidden columns) -- and the same
 // split-K over eight MFMA waves with a fixed-order reduction, but the weights
 // reach the matrix cores through LDS:
-//  * four loader waves move each unit's 32 weight rows in K-stages of KC
+//  * eight loader waves move each unit's 32 weight rows in K-stages of KC
 //    elements with gfx950's 16-byte global -> LDS loads; every load
 //    instruction reads one contiguous 1 KiB piece (one row's KC = 512
 //    elements, or two rows' 256), the pattern HBM streams fastest (6.5 TB/s
@@ -22,7 +22,7 @@
 //    task (reloaded only on a task switch, on the MFMA waves' own counter);
 //  * a unit's eight partial tiles are written to LDS after its last stage and
 //    reduced, in fixed wave order, after the next stage barrier.
-// One 768-thread workgroup per CU; persistent workgroups take blocks of
+// One 1024-thread workgroup per CU; persistent workgroups take blocks of
 // consecutive units.  Rounding as in moe_stream.hip.
 #include "common.h"
 #include "moe_internal.h"
@@ -34,7 +34,7 @@ namespace moe {
 namespace {
 
 constexpr int kConsumers = 8;
-constexpr int kLoaders = 4;
+constexpr int kLoaders = 8;
 constexpr int kThreads = (kConsumers + kLoaders) * kWave;
 constexpr int kRows = 32;  // weight rows per unit
 constexpr int kWaitVmcntZero = (7 << 4) | (15 << 8);
