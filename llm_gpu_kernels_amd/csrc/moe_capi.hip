@@ -33,10 +33,17 @@ int hip_fail(hipError_t e, const char *what) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Router fused into the planner's single workgroup up to one token per wave
-// (16); beyond that the standalone one-wave-per-token launch routes all
-// tokens in parallel across CUs, which is faster than further serial rounds.
-constexpr int kFuseRouterTokens = 16;
+// Router fused into the planner's single workgroup while one round of its 16
+// waves routes every token: one token per wave up to 16 tokens, two per wave
+// (32 lanes each, E <= 128) up to 32.  Beyond that the standalone
+// one-wave-per-token launch routes all tokens in parallel across CUs, which
+// is faster than further serial rounds.
+int fuse_router_mode(const moe_desc *d) {
+  if (d->route_mode != MOE_ROUTE_LOGITS) return 0;
+  if (d->T <= 16) return 1;
+  if (d->T <= 32 && d->E <= 128) return 2;
+  return 0;
+}
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -121,7 +128,7 @@ moe_layout compute_layout(const moe_desc *d) {
   L.total = o;
   L.task_capacity = (int32_t)cap;
   L.token_block = tb;
-  const bool fuse = d->route_mode == MOE_ROUTE_LOGITS && d->T <= kFuseRouterTokens;
+  const bool fuse = fuse_router_mode(d) != 0;
   L.fast_path = choose_path(d, tb);
   if (d->T == 0)
     L.launches = 0;
@@ -147,7 +154,7 @@ struct moe_plan {
   moe_layout L;
   int device;
   int num_cus;
-  bool fuse_router;
+  int fuse_router;  // 0: router launch, 1: one token per planner wave, 2: two
   int path;
 };
 
@@ -202,7 +209,7 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
   p->L = L;
   p->L.fast_path = path;
   p->path = path;
-  p->fuse_router = d->route_mode == MOE_ROUTE_LOGITS && d->T <= kFuseRouterTokens;
+  p->fuse_router = fuse_router_mode(d);
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess)
     e = hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, p->device);

@@ -137,6 +137,96 @@ __device__ void route_token(const float *__restrict__ logits, int t, int E, int 
   }
 }
 
+// Half-wave reductions: every lane gets the result over its 32-lane half
+// (DPP within each 16-lane row, then the gfx950 row-pair swap).
+__device__ __forceinline__ uint32_t half_umax(uint32_t v) {
+  v = umax_(v, dpp_u<0xb1>(v));
+  v = umax_(v, dpp_u<0x4e>(v));
+  v = umax_(v, dpp_u<0x141>(v));
+  v = umax_(v, dpp_u<0x140>(v));
+  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return umax_(q[0], q[1]);
+}
+__device__ __forceinline__ float half_fsum(float x) {
+  uint32_t v = __float_as_uint(x);
+  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0xb1>(v)));
+  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x4e>(v)));
+  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x141>(v)));
+  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x140>(v)));
+  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// route_token for two tokens per wave (E <= 128): half h = lane / 32 routes
+// token t of its own; expert e lives in lane 32h + e % 32, slot e / 32.  The
+// same selection (by logit, ties to the lower expert) and probabilities; a
+// half with live == false computes on -inf logits and stores nothing.
+__device__ void route_token_half(const float *__restrict__ logits, int t, bool live, int E, int K,
+                                 int renormalize, int32_t *__restrict__ ids_out,
+                                 float *__restrict__ w_out, uint32_t &flags, int *lds_ids,
+                                 float *lds_w) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = lane & 31;
+  const bool upper = lane >= 32;
+  float raw[4];
+  uint32_t key[4];
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = h + 32 * j;
+    const bool ok = live && e < E;
+    raw[j] = ok ? logits[(size_t)t * E + e] : -INFINITY;
+    bad |= ok && !isfinite(raw[j]);
+    key[j] = ok ? float_key(raw[j]) : 0u;
+  }
+  if (__any(bad)) flags |= 4u;
+  const uint32_t top = umax_(umax_(key[0], key[1]), umax_(key[2], key[3]));
+  const float m = key_float(half_umax(top));
+  float z = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (live && h + 32 * j < E) z += expf(raw[j] - m);
+  z = half_fsum(z);
+
+  uint32_t taken = 0, my_key = 0;
+  int my_id = 0;
+  for (int k = 0; k < K; ++k) {
+    uint32_t best = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (!((taken >> j) & 1)) best = umax_(best, key[j]);
+    const uint32_t M = half_umax(best);
+    int idx_lo = kMaxExperts, idx_hi = kMaxExperts;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {  // lowest slot wins: scan from the top down
+      const uint64_t hit = __ballot(live && h + 32 * j < E && !((taken >> j) & 1) && key[j] == M);
+      const uint32_t lo = (uint32_t)hit, hi = (uint32_t)(hit >> 32);
+      idx_lo = lo ? 32 * j + (int)__builtin_ctz(lo) : idx_lo;
+      idx_hi = hi ? 32 * j + (int)__builtin_ctz(hi) : idx_hi;
+    }
+    const int idx = upper ? idx_hi : idx_lo;
+    if ((idx & 31) == h) taken |= 1u << (idx / 32);
+    if (h == k) {
+      my_key = M;
+      my_id = idx;
+    }
+  }
+  const float p = h < K ? expf(key_float(my_key) - m) / z : 0.f;
+  float psum = 0.f;
+  const int base = upper ? 32 : 0;
+  for (int k = 0; k < K; ++k) psum += __shfl(p, base + k, kWave);  // slot order
+  if (live && h < K) {
+    const int q = t * K + h;
+    const float w = renormalize ? p / psum : p;
+    ids_out[q] = my_id;
+    w_out[q] = w;
+    if (lds_ids) {
+      lds_ids[q] = my_id;
+      lds_w[q] = w;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   uint32_t flags = 0;
@@ -148,7 +238,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
 
 // Routes held in LDS by the planner (covers T = 1024 at top-8).
 constexpr int kLdsRoutes = 8192;
-static_assert(16 * 32 <= kLdsRoutes, "fused router (T <= 16, K <= 32) must fit the LDS routes");
+static_assert(32 * 32 <= kLdsRoutes, "fused router (T <= 32, K <= 32) must fit the LDS routes");
 
 // LDS of the planner, carved by hand so the route arrays exist only when the
 // routes fit (R <= kLdsRoutes).
@@ -182,7 +272,13 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
 
   bool ids_in_lds = false;
   if (a.route_logits) {
-    if (LDSR && a.fuse_router) {  // the host fuses only T <= 16: one token per wave
+    if (LDSR && a.fuse_router == 2) {  // T <= 32, E <= 128: two tokens per wave
+      const int t = 2 * wave + (lane >> 5);
+      if (2 * wave < a.T)
+        route_token_half(a.logits, t, t < a.T, E, a.K, a.renormalize, (int32_t *)a.ids,
+                         a.weights, flags, s_ids, s_w);
+      ids_in_lds = true;
+    } else if (LDSR && a.fuse_router) {  // T <= 16: one token per wave
       for (int t = wave; t < a.T; t += kPlanWaves)
         route_token(a.logits, t, E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
                     s_ids, s_w);

@@ -79,6 +79,12 @@ def test_layout_for_qwen_shape():
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16))
     assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17))
+    assert lay.launches == 4  # two tokens per planner wave (E <= 128)
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=32))
+    assert lay.launches == 4
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=33))
+    assert lay.launches == 5
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, E=256))
     assert lay.launches == 5
     rc, lay = _layout(_desc(H=33, I=19, E=8, K=2))
     assert rc == 0 and lay.fast_path == 0

@@ -317,3 +317,31 @@ def test_non_default_stream(gpu_device):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     assert torch.equal(base.view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens,experts,k", [(17, 128, 8), (32, 128, 8), (31, 60, 1), (20, 8, 2),
+                                              (25, 128, 32), (16, 100, 3), (18, 33, 5)])
+def test_fused_router_two_tokens_per_wave(tokens, experts, k, gpu_device):
+    """The planner routes 17..32 tokens two per wave when E <= 128 (and one per
+    wave up to 16): IDs bit-exact with the oracle's top-k on logits full of ties
+    (ties go to the lower expert), weights to fp32 rounding, the layer within
+    tolerance, and a NaN logit raises status bit 2."""
+    x, gu, dn, _, _ = O.make_inputs(tokens=tokens, experts=experts, topk=k, hidden=128,
+                                    intermediate=128, id_dtype=torch.int32, pattern="random",
+                                    seed=tokens + experts)
+    g = torch.Generator().manual_seed(7 * tokens + k)
+    logits = torch.randint(-6, 6, (tokens, experts), generator=g).float() * 0.75
+    plan = prepare_routed_moe(*_to(gpu_device, x, logits, gu, dn), k)
+    assert plan.launches[0] != "router"
+    out = plan.forward()
+    torch.cuda.synchronize()
+    ids, w = O.route_topk(logits, k)
+    assert torch.equal(plan.ids.cpu(), ids), "router IDs differ"
+    assert torch.allclose(plan.routing_weights.cpu(), w, rtol=2e-6, atol=1e-7)
+    _check_dispatch(plan, ids, experts)
+    m = O.error(out, O.moe_reference(x, gu, dn, ids, w))
+    assert m["passed"], m
+    assert plan.read_status() == 0
+    plan.logits[tokens - 1, experts // 2] = float("nan")
+    plan.forward()
+    assert plan.read_status() & 4
