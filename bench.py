@@ -330,6 +330,7 @@ def main():
                    "weights": main_res["weights"], "routing": spec["routing"],
                    "router": "on-GPU softmax-topk-renorm", "parallelism": "single-gpu"},
         "us_per_layer": main_res["us_per_layer"],
+        "stage_us": main_res["stage_us"],
         "roofline": {"bound": "hbm", "kernel": "gate_up_swiglu", "achieved": gu["gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(args.workload), "avg_us": gu["us"],
