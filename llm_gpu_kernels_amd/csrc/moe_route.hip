@@ -23,42 +23,12 @@ constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / kWave;
 constexpr int kMaxExperts = 256;
 
-// Wave-wide reductions from DPP row permutes (quad xor 1, quad xor 2, half-row
-// mirror, row mirror) and four v_readlane: every lane gets the result.
+// DPP row permute of one dword (quad xor 1 = 0xb1, quad xor 2 = 0x4e, half-row
+// mirror = 0x141, row mirror = 0x140).
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
 }
-#define MOE_DPP_REDUCE(T, OP, TOBITS, FROMBITS)                                   \
-  v = OP(v, FROMBITS(dpp_u<0xb1>(TOBITS(v))));                                     \
-  v = OP(v, FROMBITS(dpp_u<0x4e>(TOBITS(v))));                                     \
-  v = OP(v, FROMBITS(dpp_u<0x141>(TOBITS(v))));                                    \
-  v = OP(v, FROMBITS(dpp_u<0x140>(TOBITS(v))));                                    \
-  {                                                                               \
-    const T a0 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 0));  \
-    const T a1 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 16)); \
-    const T a2 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 32)); \
-    const T a3 = FROMBITS((uint32_t)__builtin_amdgcn_readlane((int)TOBITS(v), 48)); \
-    v = OP(OP(a0, a1), OP(a2, a3));                                               \
-  }
-#define MOE_ID(x) (x)
-__device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
-__device__ __forceinline__ uint32_t umin_(uint32_t a, uint32_t b) { return a < b ? a : b; }
-__device__ __forceinline__ float fadd_(float a, float b) { return a + b; }
-__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
-  MOE_DPP_REDUCE(uint32_t, umax_, MOE_ID, MOE_ID)
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_umin(uint32_t v) {
-  MOE_DPP_REDUCE(uint32_t, umin_, MOE_ID, MOE_ID)
-  return v;
-}
-__device__ __forceinline__ float wave_fsum(float v) {
-  MOE_DPP_REDUCE(float, fadd_, __float_as_uint, __uint_as_float)
-  return v;
-}
-#undef MOE_DPP_REDUCE
-#undef MOE_ID
 
 // Order-preserving map of a float to uint32 (NaN -> 0, below -inf).
 __device__ __forceinline__ uint32_t float_key(float f) {
@@ -70,151 +40,131 @@ __device__ __forceinline__ float key_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// One wave routes token t.  Expert e lives in lane e % 64, slot e / 64.
-// Selection is by logit (softmax is monotone): K rounds of a DPP wave max
-// over the remaining keys; the lowest expert holding the max is the first
-// set bit of the first non-empty per-slot ballot (slot j holds experts
-// 64j + lane), all scalar.  Lane k keeps the key and expert of slot k and
-// the probabilities are formed once, after the loop.  NaN logits rank below
-// every number and set the logit flag.  Results go to global memory and,
-// when `lds_ids` is given, to LDS for the planner.
-__device__ void route_token(const float *__restrict__ logits, int t, int E, int K,
-                            int renormalize, int32_t *__restrict__ ids_out,
-                            float *__restrict__ w_out, uint32_t &flags, int *lds_ids,
-                            float *lds_w) {
-  const int lane = threadIdx.x & (kWave - 1);
-  float raw[4];
-  uint32_t key[4];
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + kWave * j;
-    raw[j] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
-    bad |= e < E && !isfinite(raw[j]);
-    key[j] = e < E ? float_key(raw[j]) : 0u;
-  }
-  if (__any(bad)) flags |= 4u;
-  const uint32_t top = umax_(umax_(key[0], key[1]), umax_(key[2], key[3]));
-  const float m = key_float(wave_umax(top));
-  float z = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (lane + kWave * j < E) z += expf(raw[j] - m);
-  z = wave_fsum(z);
-
-  uint32_t taken = 0, my_key = 0;
-  int my_id = 0;
-  for (int k = 0; k < K; ++k) {
-    uint32_t best = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (!((taken >> j) & 1)) best = umax_(best, key[j]);
-    const uint32_t M = wave_umax(best);
-    int idx = kMaxExperts;
-#pragma unroll
-    for (int j = 3; j >= 0; --j) {  // lowest slot wins: scan from the top down
-      const uint64_t hit = __ballot(lane + kWave * j < E && !((taken >> j) & 1) && key[j] == M);
-      idx = hit ? kWave * j + (int)__builtin_ctzll(hit) : idx;
-    }
-    if ((idx & (kWave - 1)) == lane) taken |= 1u << (idx / kWave);
-    if (lane == k) {
-      my_key = M;
-      my_id = idx;
-    }
-  }
-  const float p = lane < K ? expf(key_float(my_key) - m) / z : 0.f;
-  float psum = 0.f;
-  for (int k = 0; k < K; ++k) psum += __shfl(p, k, kWave);  // slot order, every lane alike
-  if (lane < K) {
-    const int q = t * K + lane;
-    const float w = renormalize ? p / psum : p;
-    ids_out[q] = my_id;
-    w_out[q] = w;
-    if (lds_ids) {
-      lds_ids[q] = my_id;
-      lds_w[q] = w;
-    }
-  }
-}
-
-// Half-wave reductions: every lane gets the result over its 32-lane half
-// (DPP within each 16-lane row, then the gfx950 row-pair swap).
-__device__ __forceinline__ uint32_t half_umax(uint32_t v) {
-  v = umax_(v, dpp_u<0xb1>(v));
-  v = umax_(v, dpp_u<0x4e>(v));
-  v = umax_(v, dpp_u<0x141>(v));
-  v = umax_(v, dpp_u<0x140>(v));
-  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return umax_(q[0], q[1]);
-}
-__device__ __forceinline__ float half_fsum(float x) {
+// Reductions over the lanes routing one token: the whole wave (HALF =
+// false) or each 32-lane half (HALF = true): DPP within 16-lane rows, then
+// gfx950's row-pair and half swaps; every lane of the group gets the result.
+// The float sum adds rows as (r0 + r1) + (r2 + r3).
+template <bool HALF>
+__device__ __forceinline__ float group_fsum(float x) {
   uint32_t v = __float_as_uint(x);
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0xb1>(v)));
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x4e>(v)));
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x141>(v)));
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x140>(v)));
   const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+  v = __float_as_uint(__uint_as_float(q[0]) + __uint_as_float(q[1]));
+  if (!HALF) {
+    const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = __float_as_uint(__uint_as_float(h[0]) + __uint_as_float(h[1]));
+  }
+  return __uint_as_float(v);
+}
+// Inclusive prefix sum over the wave: DPP row shifts, then row broadcasts
+// (lane 15 into rows 1 and 3, lane 31 into rows 2 and 3).
+template <int CTRL, int ROWS = 0xf, int BANKS = 0xf>
+__device__ __forceinline__ int dpp_add(int v, int src) {
+  return v + __builtin_amdgcn_update_dpp(0, src, CTRL, ROWS, BANKS, false);
+}
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  int v = dpp_add<0x111>(x, x);           // row_shr:1
+  v = dpp_add<0x112>(v, x);               // row_shr:2
+  v = dpp_add<0x113>(v, x);               // row_shr:3
+  v = dpp_add<0x114, 0xf, 0xe>(v, v);     // row_shr:4, banks 1-3
+  v = dpp_add<0x118, 0xf, 0xc>(v, v);     // row_shr:8, banks 2-3
+  v = dpp_add<0x142, 0xa, 0xf>(v, v);     // row_bcast:15 into rows 1, 3
+  v = dpp_add<0x143, 0xc, 0xf>(v, v);     // row_bcast:31 into rows 2, 3
+  return v;
 }
 
-// route_token for two tokens per wave (E <= 128): half h = lane / 32 routes
-// token t of its own; expert e lives in lane 32h + e % 32, slot e / 32.  The
-// same selection (by logit, ties to the lower expert) and probabilities; a
-// half with live == false computes on -inf logits and stores nothing.
-__device__ void route_token_half(const float *__restrict__ logits, int t, bool live, int E, int K,
-                                 int renormalize, int32_t *__restrict__ ids_out,
-                                 float *__restrict__ w_out, uint32_t &flags, int *lds_ids,
-                                 float *lds_w) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int h = lane & 31;
-  const bool upper = lane >= 32;
-  float raw[4];
+template <bool HALF, bool MAX>
+__device__ __forceinline__ uint32_t group_uext(uint32_t v) {
+  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  v = op(v, dpp_u<0xb1>(v));
+  v = op(v, dpp_u<0x4e>(v));
+  v = op(v, dpp_u<0x141>(v));
+  v = op(v, dpp_u<0x140>(v));
+  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = op(q[0], q[1]);
+  if (!HALF) {
+    const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(h[0], h[1]);
+  }
+  return v;
+}
+
+// Logits of token t for one lane: expert e = h + L j (j < 4) with L = 64
+// lanes per token (h = lane) or L = 32 (HALF: h = lane % 32, token of the
+// half).  Issued early so the planner's set-up hides their latency.
+template <bool HALF>
+__device__ __forceinline__ void load_token_logits(const float *__restrict__ logits, int t, bool live,
+                                                  int E, float (&raw)[4]) {
+  constexpr int L = HALF ? 32 : 64;
+  const int h = threadIdx.x & (L - 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = h + L * j;
+    raw[j] = live && e < E ? logits[(size_t)t * E + e] : -INFINITY;
+  }
+}
+
+// The lanes of one token route it from its logits (raw, as loaded above).
+// Selection is by logit (softmax is monotone): K rounds of a group max over
+// each lane's best remaining key, then a group min over the experts holding
+// that key (equal logits go to the lower expert), whose lane drops it.  Keys
+// are offset by one so a dropped or absent expert (0) ranks below a NaN
+// logit (1).  Lane k keeps the key and expert of slot k and the
+// probabilities are formed once, after the loop.  NaN logits rank below
+// every number and set the logit flag.  Results go to global memory and,
+// when `lds_ids` is given, to LDS for the planner.  A group with live ==
+// false computes on nothing and stores nothing.
+template <bool HALF>
+__device__ void route_token(const float (&raw)[4], int t, bool live, int E, int K, int renormalize,
+                            int32_t *__restrict__ ids_out, float *__restrict__ w_out,
+                            uint32_t &flags, int *lds_ids, float *lds_w) {
+  constexpr int L = HALF ? 32 : 64;
+  const int h = threadIdx.x & (L - 1);
   uint32_t key[4];
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int e = h + 32 * j;
-    const bool ok = live && e < E;
-    raw[j] = ok ? logits[(size_t)t * E + e] : -INFINITY;
+    const bool ok = live && h + L * j < E;
     bad |= ok && !isfinite(raw[j]);
-    key[j] = ok ? float_key(raw[j]) : 0u;
+    key[j] = ok ? float_key(raw[j]) + 1u : 0u;
   }
   if (__any(bad)) flags |= 4u;
-  const uint32_t top = umax_(umax_(key[0], key[1]), umax_(key[2], key[3]));
-  const float m = key_float(half_umax(top));
+  auto top4 = [&]() {
+    const uint32_t a = key[0] > key[1] ? key[0] : key[1], b = key[2] > key[3] ? key[2] : key[3];
+    return a > b ? a : b;
+  };
+  const uint32_t kmax = group_uext<HALF, true>(top4());
+  const float m = key_float(kmax - 1u);
   float z = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (live && h + 32 * j < E) z += expf(raw[j] - m);
-  z = half_fsum(z);
+    if (live && h + L * j < E) z += expf(raw[j] - m);
+  z = group_fsum<HALF>(z);
 
-  uint32_t taken = 0, my_key = 0;
-  int my_id = 0;
+  uint32_t my_key = 1;
+  int my_id = kMaxExperts;
   for (int k = 0; k < K; ++k) {
-    uint32_t best = 0;
+    const uint32_t M = group_uext<HALF, true>(top4());
+    uint32_t c = kMaxExperts;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (!((taken >> j) & 1)) best = umax_(best, key[j]);
-    const uint32_t M = half_umax(best);
-    int idx_lo = kMaxExperts, idx_hi = kMaxExperts;
+    for (int j = 3; j >= 0; --j)
+      if (M != 0 && key[j] == M) c = h + L * j;
+    const int idx = (int)group_uext<HALF, false>(c);
+    if (idx < kMaxExperts && (idx & (L - 1)) == h) {
 #pragma unroll
-    for (int j = 3; j >= 0; --j) {  // lowest slot wins: scan from the top down
-      const uint64_t hit = __ballot(live && h + 32 * j < E && !((taken >> j) & 1) && key[j] == M);
-      const uint32_t lo = (uint32_t)hit, hi = (uint32_t)(hit >> 32);
-      idx_lo = lo ? 32 * j + (int)__builtin_ctz(lo) : idx_lo;
-      idx_hi = hi ? 32 * j + (int)__builtin_ctz(hi) : idx_hi;
+      for (int j = 0; j < 4; ++j)
+        if (idx / L == j) key[j] = 0;
     }
-    const int idx = upper ? idx_hi : idx_lo;
-    if ((idx & 31) == h) taken |= 1u << (idx / 32);
     if (h == k) {
       my_key = M;
       my_id = idx;
     }
   }
-  const float p = h < K ? expf(key_float(my_key) - m) / z : 0.f;
-  float psum = 0.f;
-  const int base = upper ? 32 : 0;
-  for (int k = 0; k < K; ++k) psum += __shfl(p, base + k, kWave);  // slot order
+  const float p = h < K ? expf(key_float(my_key - 1u) - m) / z : 0.f;
+  const float psum = group_fsum<HALF>(p);
   if (live && h < K) {
     const int q = t * K + h;
     const float w = renormalize ? p / psum : p;
@@ -230,9 +180,12 @@ __device__ void route_token_half(const float *__restrict__ logits, int t, bool l
 __global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   uint32_t flags = 0;
-  if (t < a.T)
-    route_token(a.logits, t, a.E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
-                nullptr, nullptr);
+  if (t < a.T) {
+    float raw[4];
+    load_token_logits<false>(a.logits, t, true, a.E, raw);
+    route_token<false>(raw, t, true, a.E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
+                       nullptr, nullptr);
+  }
   if (flags && (threadIdx.x & 63) == 0) atomicOr(&a.status[1], flags);
 }
 
@@ -265,6 +218,14 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   const int wave = tid >> 6;
   const int lane = tid & (kWave - 1);
   const int E = a.E;
+  // Fused router: one token per wave (mode 1, T <= 16) or per half-wave
+  // (mode 2, T <= 32, E <= 128); the logits are requested before the set-up.
+  const int fmode = LDSR && a.route_logits ? a.fuse_router : 0;
+  const int ft = fmode == 2 ? 2 * wave + (lane >> 5) : wave;
+  const bool fwave = fmode == 2 ? 2 * wave < a.T : wave < a.T;  // wave-uniform
+  float raw[4];
+  if (fmode == 2) load_token_logits<true>(a.logits, ft, ft < a.T, E, raw);
+  else if (fmode == 1) load_token_logits<false>(a.logits, ft, ft < a.T, E, raw);
   if (tid == 0) sh.status = 0;
   for (int e = tid; e < E; e += kPlanThreads) sh.run[e] = 0;
   for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) (&sh.wcnt[0][0][0])[i] = 0;
@@ -272,16 +233,15 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
 
   bool ids_in_lds = false;
   if (a.route_logits) {
-    if (LDSR && a.fuse_router == 2) {  // T <= 32, E <= 128: two tokens per wave
-      const int t = 2 * wave + (lane >> 5);
-      if (2 * wave < a.T)
-        route_token_half(a.logits, t, t < a.T, E, a.K, a.renormalize, (int32_t *)a.ids,
-                         a.weights, flags, s_ids, s_w);
+    if (fmode == 2) {
+      if (fwave)
+        route_token<true>(raw, ft, ft < a.T, E, a.K, a.renormalize, (int32_t *)a.ids, a.weights,
+                          flags, s_ids, s_w);
       ids_in_lds = true;
-    } else if (LDSR && a.fuse_router) {  // T <= 16: one token per wave
-      for (int t = wave; t < a.T; t += kPlanWaves)
-        route_token(a.logits, t, E, a.K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
-                    s_ids, s_w);
+    } else if (fmode == 1) {
+      if (fwave)
+        route_token<false>(raw, ft, true, E, a.K, a.renormalize, (int32_t *)a.ids, a.weights,
+                           flags, s_ids, s_w);
       ids_in_lds = true;
     } else if (tid == 0) {
       flags |= a.status[1];  // written by router_kernel earlier on this stream
@@ -425,16 +385,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
       csum += c[j];
       tsum += nt[j];
     }
-    int cinc = csum, tinc = tsum;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int cu = __shfl_up(cinc, o, kWave);
-      const int tu = __shfl_up(tinc, o, kWave);
-      if (lane >= o) {
-        cinc += cu;
-        tinc += tu;
-      }
-    }
+    const int cinc = wave_incl_scan(csum), tinc = wave_incl_scan(tsum);
     int crun = cinc - csum, trun = tinc - tsum;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
