@@ -72,7 +72,10 @@ struct DmaCfg {
   static constexpr int KKS = KC / kConsumers / 32;        // k-steps per wave per stage
   static constexpr int RED = 2 * kConsumers * 2 * MT * kWave * 16;  // partials, 2 parities
   static constexpr int NS0 = (int)((kMaxLds - RED) / STAGE);
-  static constexpr int NS = NS0 > 8 ? 8 : NS0;
+  // Ring depth: down's 16 KiB stages stream best with four ahead (measured:
+  // 0.5 us faster than seven ahead at T = 17 and 193); gate/up keeps all it fits.
+  static constexpr int NSMAX = KIND == 1 ? 5 : 8;
+  static constexpr int NS = NS0 > NSMAX ? NSMAX : NS0;
   static constexpr int PER = STAGE / 1024 / kLoaders;     // 1 KiB loads per stage per loader
   static_assert(NS >= 3, "at least two stages ahead");
   static_assert((NS - 2) * PER < 64, "vmcnt range");
