@@ -101,6 +101,19 @@ int validate(const moe_desc *d) {
   return MOE_OK;
 }
 
+// Router-fused bf16 shapes whose gate/up streams through LDS with 16-row
+// tasks plan in the gate/up prologue instead of a planner launch.
+bool planned_gate_up(const moe_desc *d, int path, int tb) {
+  return path == moe::kStream && tb == 16 && d->weight_format != MOE_WEIGHTS_W4G128 &&
+         moe::dma_plan_ok(d->H, d->I, d->T, d->K, d->E, fuse_router_mode(d));
+}
+
+int launch_count(const moe_desc *d, int path, int tb) {
+  if (d->T == 0) return 0;
+  if (planned_gate_up(d, path, tb)) return 3;  // gate/up (planning), down, combine
+  return 4 + (d->route_mode == MOE_ROUTE_LOGITS && fuse_router_mode(d) == 0 ? 1 : 0);
+}
+
 moe_layout compute_layout(const moe_desc *d) {
   moe_layout L;
   memset(&L, 0, sizeof(L));
@@ -128,12 +141,8 @@ moe_layout compute_layout(const moe_desc *d) {
   L.total = o;
   L.task_capacity = (int32_t)cap;
   L.token_block = tb;
-  const bool fuse = fuse_router_mode(d) != 0;
   L.fast_path = choose_path(d, tb);
-  if (d->T == 0)
-    L.launches = 0;
-  else
-    L.launches = 4 + (d->route_mode == MOE_ROUTE_LOGITS && !fuse ? 1 : 0);
+  L.launches = launch_count(d, L.fast_path, tb);
   return L;
 }
 
@@ -155,6 +164,7 @@ struct moe_plan {
   int device;
   int num_cus;
   int fuse_router;  // 0: router launch, 1: one token per planner wave, 2: two
+  bool planned;     // gate/up routes and plans in its prologue (no planner launch)
   int path;
 };
 
@@ -210,6 +220,8 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
   p->L.fast_path = path;
   p->path = path;
   p->fuse_router = fuse_router_mode(d);
+  p->planned = planned_gate_up(d, path, L.token_block);
+  p->L.launches = launch_count(d, path, L.token_block);
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess)
     e = hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
@@ -228,7 +240,7 @@ int moe_plan_layout(const moe_plan *p, moe_layout *out) {
 }
 
 // Launch stages [first, last) of one forward.  Stage order:
-// [router] route_plan gate_up down combine.
+// [router] route_plan gate_up down combine, or gate_up (planning) down combine.
 static int run_stages(moe_plan *p, int first, int last, void *stream) {
   const moe_desc &d = p->d;
   if (d.T == 0) return MOE_OK;
@@ -292,7 +304,8 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   const bool router = ra.route_logits && !ra.fuse_router;
   int rc = MOE_OK;
   for (int st = first; st < last && rc == MOE_OK; ++st) {
-    const int kind = router ? st : st + 1;  // 0 router, 1 plan, 2 gate/up, 3 down, 4 combine
+    // 0 router, 1 plan, 2 gate/up, 3 down, 4 combine, 5 gate/up with the plan
+    const int kind = p->planned ? (st == 0 ? 5 : st + 2) : router ? st : st + 1;
     switch (kind) {
       case 0: e = moe::launch_router(ra, s); break;
       case 1: e = moe::launch_route_plan(ra, s); break;
@@ -302,10 +315,11 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
       case 3:
         e = moe::launch_down(xa, L.task_capacity, L.token_block, p->path, p->num_cus, s);
         break;
-      default: e = moe::launch_combine(xa, s); break;
+      case 4: e = moe::launch_combine(xa, s); break;
+      default: e = moe::launch_dma_gate_up_planned(xa, ra, p->num_cus, s); break;
     }
     if (e != hipSuccess) {
-      static const char *names[] = {"router", "route plan", "gate/up", "down", "combine"};
+      static const char *names[] = {"router", "route plan", "gate/up", "down", "combine", "gate/up"};
       rc = hip_fail(e, names[kind]);
     }
   }

@@ -26,6 +26,7 @@
 // consecutive units.  Rounding as in moe_stream.hip.
 #include "common.h"
 #include "moe_internal.h"
+#include "moe_route_dev.h"
 
 #define MOE_CONST __attribute__((address_space(4)))
 
@@ -65,13 +66,24 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int KIND, int MT>
+// Planning prologue (PLAN): the task list and grouped-row -> token table stay
+// in LDS for the whole launch.
+constexpr int kPlanTaskMax = route_dev::kMaxExperts + route_dev::kSmallPlanRoutes / 16;
+constexpr int kPlanBytes = kPlanTaskMax * 16 + (route_dev::kSmallPlanRoutes + 64) * 4 + 16;
+
+template <int KIND, int MT, bool PLAN = false>
 struct DmaCfg {
   static constexpr int KC = KIND == 0 ? 512 : 256;      // K per stage
   static constexpr int STAGE = kRows * KC * 2;            // bytes
   static constexpr int KKS = KC / kConsumers / 32;        // k-steps per wave per stage
-  static constexpr int RED = 2 * kConsumers * 2 * MT * kWave * 16;  // partials, 2 parities
-  static constexpr int NS0 = (int)((kMaxLds - RED) / STAGE);
+  // Partial tiles: two buffers by unit parity; one suffices with two or more
+  // stages per unit (always so for PLAN): the next unit writes its partials
+  // only after its second stage barrier, which every wave reaches after its
+  // part of the reduction.
+  static constexpr int PAR = PLAN ? 1 : 2;
+  static constexpr int RED = PAR * kConsumers * 2 * MT * kWave * 16;
+  static constexpr int PLANB = PLAN ? kPlanBytes : 0;
+  static constexpr int NS0 = (int)((kMaxLds - RED - PLANB) / STAGE);
   // Ring depth: down's 16 KiB stages stream best with four ahead (measured:
   // 0.5 us faster than seven ahead at T = 17 and 193); gate/up keeps all it fits.
   static constexpr int NSMAX = KIND == 1 ? 5 : 8;
@@ -87,9 +99,15 @@ __device__ __forceinline__ int stage_off(int R, int c) {
   return R * (KC * 2) + ((c ^ (R & 15)) << 4);
 }
 
-template <int KIND, int MT, int SPU>
-__global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
-  using C = DmaCfg<KIND, MT>;
+// PLAN (gate/up, 16-row tasks, T <= 32 router-fused shapes): every workgroup
+// first routes all tokens and plans in LDS (route_dev::route_token and
+// plan_small), and workgroup 0 also writes the routing results and the global
+// plan arrays for the down and combine launches; the separate planner launch
+// is then not needed.
+template <int KIND, int MT, int SPU, bool PLAN = false>
+__global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs ra) {
+  using C = DmaCfg<KIND, MT, PLAN>;
+  static_assert(!PLAN || (KIND == 0 && MT == 1 && SPU >= 2), "planning prologue: 16-row gate/up");
   constexpr int KC = C::KC, KKS = C::KKS, NS = C::NS, PER = C::PER;
   constexpr int NRB = 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -101,7 +119,52 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
   const int H = a.H, I = a.I;
   const int K = KIND == 0 ? H : I;  // == SPU * KC (checked on the host)
   const int ncb = KIND == 0 ? I / 16 : H / 32;  // units per task
-  const int total = *as_const(a.num_tasks) * ncb;
+  const int4 *l_tasks = nullptr;
+  const int *l_row_token = nullptr;
+  int ntasks = 0;
+  if constexpr (PLAN) {
+    using namespace route_dev;
+    uint8_t *pa = smem + NS * C::STAGE + C::RED;
+    int4 *p_tasks = (int4 *)pa;
+    int *p_row = (int *)(pa + kPlanTaskMax * 16);
+    int *p_nt = p_row + kSmallPlanRoutes + 64;
+    // Scratch in the (still idle) stage ring.
+    int *x_ids = (int *)smem;
+    float *x_w = (float *)(smem + 4 * kSmallPlanRoutes);
+    int *x_wcnt = (int *)(smem + 8 * kSmallPlanRoutes);
+    int *x_cnt = x_wcnt + kSmallPlanWaves * kMaxExperts;
+    int *x_off = x_cnt + kMaxExperts;
+    int *x_toff = x_off + kMaxExperts;
+    uint32_t *x_flags = (uint32_t *)(x_toff + kMaxExperts + 1);
+    // One token per wave (fuse_router 1) or half-wave (2); logits first.
+    const bool half = ra.fuse_router == 2;
+    const int ft = half ? 2 * wave + (lane >> 5) : wave;
+    const bool fwave = half ? 2 * wave < ra.T : wave < ra.T;  // wave-uniform
+    float raw[4];
+    if (half) load_token_logits<true>(ra.logits, ft, ft < ra.T, ra.E, raw);
+    else load_token_logits<false>(ra.logits, ft, ft < ra.T, ra.E, raw);
+    for (int i = tid; i < kSmallPlanWaves * ra.E; i += kThreads) x_wcnt[i] = 0;
+    if (tid == 0) *x_flags = 0;
+    const bool g0 = blockIdx.x == 0;
+    uint32_t flags = 0;
+    if (fwave) {
+      int32_t *ids_g = g0 ? (int32_t *)ra.ids : nullptr;
+      float *w_g = g0 ? ra.weights : nullptr;
+      if (half)
+        route_token<true>(raw, ft, ft < ra.T, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+      else
+        route_token<false>(raw, ft, true, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+    }
+    __syncthreads();
+    const SmallPlanLds L{x_ids, x_w, x_wcnt, x_cnt, x_off, x_toff, p_tasks, p_row, p_nt, x_flags};
+    const SmallPlanOut O{ra.counts, ra.offsets, ra.ranks, ra.map, ra.row_route, ra.row_token,
+                         ra.tasks, ra.num_tasks, ra.counters, ra.status};
+    plan_small(L, O, g0, ra.R, ra.E, ra.K, 16, flags);
+    ntasks = *p_nt;
+    l_tasks = p_tasks;
+    l_row_token = p_row;
+  }
+  const int total = (PLAN ? ntasks : *as_const(a.num_tasks)) * ncb;
   const int G = gridDim.x;
   const int cper = (total + G - 1) / G;
   const int b0 = (int)blockIdx.x * cper;
@@ -120,9 +183,24 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
     const int lrow = lane / LPR, lch = lane % LPR;
     int cur = -1;
     const uint16_t *src[PER];
+    // The task's expert: from LDS with PLAN through an instruction the compiler
+    // cannot see (a visible LDS access after global -> LDS loads makes it
+    // wait for every such load in flight).
+    auto expert_of = [&](int t) -> int {
+      if constexpr (PLAN) {
+        uint32_t v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                     : "=v"(v)
+                     : "v"((uint32_t)(size_t)(const __attribute__((address_space(3))) int4 *)(l_tasks + t))
+                     : "memory");
+        return __builtin_amdgcn_readfirstlane(v);
+      } else {
+        return tasks[4 * t];
+      }
+    };
     auto setup = [&](int u) {
       const int t = u / ncb, cb = u - t * ncb;
-      const int e = tasks[4 * t];
+      const int e = expert_of(t);
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         const int R = (lw * PER + j) * RPI + lrow;  // stage row
@@ -178,9 +256,16 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
     Meta m;
     m.task = u / ncb;
     m.cb = u - m.task * ncb;
-    m.row0 = tasks[4 * m.task + 1];
-    m.rows = tasks[4 * m.task + 2];
-    m.idxv = row_vec[m.row0 + (lane & 31)];
+    if constexpr (PLAN) {
+      const int4 tk = l_tasks[m.task];
+      m.row0 = __builtin_amdgcn_readfirstlane(tk.y);
+      m.rows = __builtin_amdgcn_readfirstlane(tk.z);
+      m.idxv = l_row_token[m.row0 + (lane & 31)];
+    } else {
+      m.row0 = tasks[4 * m.task + 1];
+      m.rows = tasks[4 * m.task + 2];
+      m.idxv = row_vec[m.row0 + (lane & 31)];
+    }
     return m;
   };
 
@@ -262,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
 #pragma unroll
     for (int s = 0; s < SPU; ++s, ++st) {
       lds_barrier();  // stage st published; unit i-1's partials published
-      if (s == 0 && i > 0) epilogue(prev, (i - 1) & 1);
+      if (s == 0 && i > 0) epilogue(prev, (i - 1) % C::PAR);
       const uint8_t *buf = smem + (st % NS) * C::STAGE;
       u32x4 af[KKS][NRB];
 #pragma unroll
@@ -280,8 +365,8 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
           for (int mt = 0; mt < MT; ++mt)
             acc[rb][mt] = mfma16(af[kk][rb], bfr[mt][s * KKS + kk], acc[rb][mt]);
     }
-    // Partials of unit i (parity i & 1), reduced after the next barrier.
-    f32x4 *red = s_red + (size_t)(i & 1) * kConsumers * NRB * MT * kWave;
+    // Partials of unit i (buffer i % PAR), reduced after the next barrier.
+    f32x4 *red = s_red + (size_t)(i % C::PAR) * kConsumers * NRB * MT * kWave;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
@@ -289,19 +374,20 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a) {
     prev = cur;
   }
   lds_barrier();
-  epilogue(prev, (count - 1) & 1);
+  epilogue(prev, (count - 1) % C::PAR);
 }
 
-template <int KIND, int MT, int SPU>
-hipError_t launch_one(const ExpertArgs &a, int num_cus, hipStream_t s) {
-  using C = DmaCfg<KIND, MT>;
-  auto k = dma_kernel<KIND, MT, SPU>;
-  const size_t lds = (size_t)C::NS * C::STAGE + C::RED;
+template <int KIND, int MT, int SPU, bool PLAN = false>
+hipError_t launch_one(const ExpertArgs &a, int num_cus, hipStream_t s, const RouteArgs *ra = nullptr) {
+  using C = DmaCfg<KIND, MT, PLAN>;
+  auto k = dma_kernel<KIND, MT, SPU, PLAN>;
+  const size_t lds = (size_t)C::NS * C::STAGE + C::RED + C::PLANB;
   static const bool attr = hipFuncSetAttribute((const void *)k,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds) == hipSuccess;
   if (!attr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k, dim3(num_cus > 0 ? num_cus : 1), dim3(kThreads), lds, s, a);
+  RouteArgs none{};
+  hipLaunchKernelGGL(k, dim3(num_cus > 0 ? num_cus : 1), dim3(kThreads), lds, s, a, ra ? *ra : none);
   return hipGetLastError();
 }
 
@@ -336,6 +422,22 @@ hipError_t launch_dma_gate_up(const ExpertArgs &a, int token_block, int num_cus,
 hipError_t launch_dma_down(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s) {
   const int spu = a.I / 256;
   return token_block == 16 ? launch_spu<1, 1>(a, spu, num_cus, s) : launch_spu<1, 2>(a, spu, num_cus, s);
+}
+
+// gate/up with the routing and planning prologue: 16-row tasks, H = 1024 or
+// 2048, at most 1024 routes, the router shapes the planner fuses (one token
+// per wave up to 16 tokens, per half-wave up to 32 with E <= 128).
+bool dma_plan_ok(int H, int I, int T, int K, int E, int fuse_router) {
+  return dma_shape_ok(H, I, 16) && (H == 1024 || H == 2048) && fuse_router != 0 &&
+         T * K <= route_dev::kSmallPlanRoutes && E <= route_dev::kMaxExperts &&
+         E + (T * K + 15) / 16 <= kPlanTaskMax;
+}
+
+hipError_t launch_dma_gate_up_planned(const ExpertArgs &a, const RouteArgs &ra, int num_cus,
+                                      hipStream_t s) {
+  if (a.H == 1024) return launch_one<0, 1, 2, true>(a, num_cus, s, &ra);
+  if (a.H == 2048) return launch_one<0, 1, 4, true>(a, num_cus, s, &ra);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace moe

@@ -59,6 +59,11 @@ bool stream_shape_ok(int H, int I, bool w4);
 bool dma_shape_ok(int H, int I, int token_block);
 hipError_t launch_dma_gate_up(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s);
 hipError_t launch_dma_down(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s);
+// The same gate/up kernel routing and planning in its prologue (replaces the
+// planner launch for router-fused shapes; writes every global plan array).
+bool dma_plan_ok(int H, int I, int T, int K, int E, int fuse_router);
+hipError_t launch_dma_gate_up_planned(const ExpertArgs &a, const RouteArgs &ra, int num_cus,
+                                      hipStream_t s);
 // W4 gate/up + SwiGLU, one unit per wave with K-chunked token rows in LDS, for
 // tasks with several rows per expert (token_block 16, 32 or 64).
 bool wave_w4_shape_ok(int H, int I, int token_block);

@@ -14,6 +14,7 @@
 // bit-identical from run to run.
 #include "common.h"
 #include "moe_internal.h"
+#include "moe_route_dev.h"
 
 namespace moe {
 
@@ -21,161 +22,7 @@ namespace {
 
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / kWave;
-constexpr int kMaxExperts = 256;
-
-// DPP row permute of one dword (quad xor 1 = 0xb1, quad xor 2 = 0x4e, half-row
-// mirror = 0x141, row mirror = 0x140).
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
-}
-
-// Order-preserving map of a float to uint32 (NaN -> 0, below -inf).
-__device__ __forceinline__ uint32_t float_key(float f) {
-  if (isnan(f)) return 0u;
-  const uint32_t b = __float_as_uint(f);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float key_float(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-// Reductions over the lanes routing one token: the whole wave (HALF =
-// false) or each 32-lane half (HALF = true): DPP within 16-lane rows, then
-// gfx950's row-pair and half swaps; every lane of the group gets the result.
-// The float sum adds rows as (r0 + r1) + (r2 + r3).
-template <bool HALF>
-__device__ __forceinline__ float group_fsum(float x) {
-  uint32_t v = __float_as_uint(x);
-  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0xb1>(v)));
-  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x4e>(v)));
-  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x141>(v)));
-  v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x140>(v)));
-  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = __float_as_uint(__uint_as_float(q[0]) + __uint_as_float(q[1]));
-  if (!HALF) {
-    const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    v = __float_as_uint(__uint_as_float(h[0]) + __uint_as_float(h[1]));
-  }
-  return __uint_as_float(v);
-}
-// Inclusive prefix sum over the wave: DPP row shifts, then row broadcasts
-// (lane 15 into rows 1 and 3, lane 31 into rows 2 and 3).
-template <int CTRL, int ROWS = 0xf, int BANKS = 0xf>
-__device__ __forceinline__ int dpp_add(int v, int src) {
-  return v + __builtin_amdgcn_update_dpp(0, src, CTRL, ROWS, BANKS, false);
-}
-__device__ __forceinline__ int wave_incl_scan(int x) {
-  int v = dpp_add<0x111>(x, x);           // row_shr:1
-  v = dpp_add<0x112>(v, x);               // row_shr:2
-  v = dpp_add<0x113>(v, x);               // row_shr:3
-  v = dpp_add<0x114, 0xf, 0xe>(v, v);     // row_shr:4, banks 1-3
-  v = dpp_add<0x118, 0xf, 0xc>(v, v);     // row_shr:8, banks 2-3
-  v = dpp_add<0x142, 0xa, 0xf>(v, v);     // row_bcast:15 into rows 1, 3
-  v = dpp_add<0x143, 0xc, 0xf>(v, v);     // row_bcast:31 into rows 2, 3
-  return v;
-}
-
-template <bool HALF, bool MAX>
-__device__ __forceinline__ uint32_t group_uext(uint32_t v) {
-  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
-  v = op(v, dpp_u<0xb1>(v));
-  v = op(v, dpp_u<0x4e>(v));
-  v = op(v, dpp_u<0x141>(v));
-  v = op(v, dpp_u<0x140>(v));
-  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = op(q[0], q[1]);
-  if (!HALF) {
-    const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    v = op(h[0], h[1]);
-  }
-  return v;
-}
-
-// Logits of token t for one lane: expert e = h + L j (j < 4) with L = 64
-// lanes per token (h = lane) or L = 32 (HALF: h = lane % 32, token of the
-// half).  Issued early so the planner's set-up hides their latency.
-template <bool HALF>
-__device__ __forceinline__ void load_token_logits(const float *__restrict__ logits, int t, bool live,
-                                                  int E, float (&raw)[4]) {
-  constexpr int L = HALF ? 32 : 64;
-  const int h = threadIdx.x & (L - 1);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = h + L * j;
-    raw[j] = live && e < E ? logits[(size_t)t * E + e] : -INFINITY;
-  }
-}
-
-// The lanes of one token route it from its logits (raw, as loaded above).
-// Selection is by logit (softmax is monotone): K rounds of a group max over
-// each lane's best remaining key, then a group min over the experts holding
-// that key (equal logits go to the lower expert), whose lane drops it.  Keys
-// are offset by one so a dropped or absent expert (0) ranks below a NaN
-// logit (1).  Lane k keeps the key and expert of slot k and the
-// probabilities are formed once, after the loop.  NaN logits rank below
-// every number and set the logit flag.  Results go to global memory and,
-// when `lds_ids` is given, to LDS for the planner.  A group with live ==
-// false computes on nothing and stores nothing.
-template <bool HALF>
-__device__ void route_token(const float (&raw)[4], int t, bool live, int E, int K, int renormalize,
-                            int32_t *__restrict__ ids_out, float *__restrict__ w_out,
-                            uint32_t &flags, int *lds_ids, float *lds_w) {
-  constexpr int L = HALF ? 32 : 64;
-  const int h = threadIdx.x & (L - 1);
-  uint32_t key[4];
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool ok = live && h + L * j < E;
-    bad |= ok && !isfinite(raw[j]);
-    key[j] = ok ? float_key(raw[j]) + 1u : 0u;
-  }
-  if (__any(bad)) flags |= 4u;
-  auto top4 = [&]() {
-    const uint32_t a = key[0] > key[1] ? key[0] : key[1], b = key[2] > key[3] ? key[2] : key[3];
-    return a > b ? a : b;
-  };
-  const uint32_t kmax = group_uext<HALF, true>(top4());
-  const float m = key_float(kmax - 1u);
-  float z = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (live && h + L * j < E) z += expf(raw[j] - m);
-  z = group_fsum<HALF>(z);
-
-  uint32_t my_key = 1;
-  int my_id = kMaxExperts;
-  for (int k = 0; k < K; ++k) {
-    const uint32_t M = group_uext<HALF, true>(top4());
-    uint32_t c = kMaxExperts;
-#pragma unroll
-    for (int j = 3; j >= 0; --j)
-      if (M != 0 && key[j] == M) c = h + L * j;
-    const int idx = (int)group_uext<HALF, false>(c);
-    if (idx < kMaxExperts && (idx & (L - 1)) == h) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (idx / L == j) key[j] = 0;
-    }
-    if (h == k) {
-      my_key = M;
-      my_id = idx;
-    }
-  }
-  const float p = h < K ? expf(key_float(my_key - 1u) - m) / z : 0.f;
-  const float psum = group_fsum<HALF>(p);
-  if (live && h < K) {
-    const int q = t * K + h;
-    const float w = renormalize ? p / psum : p;
-    ids_out[q] = my_id;
-    w_out[q] = w;
-    if (lds_ids) {
-      lds_ids[q] = my_id;
-      lds_w[q] = w;
-    }
-  }
-}
+using namespace route_dev;
 
 __global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);

@@ -8,8 +8,10 @@ moe_w4_cuda.py:85; ``prepare_w4_layout_moe``: moe_w4_layout_cuda.py:152;
 lifetime rules: docs/MOE_USAGE.md:93-146) and adds the router-inclusive
 ``prepare_routed_moe(...).forward(hidden, router_logits)``.
 
-Every forward is four or five launches of hand-written gfx950 kernels on the
-current stream: [router] -> planner -> gate/up+SwiGLU -> down -> combine.  No
+Every forward is three to five launches of hand-written gfx950 kernels on the
+current stream: [router] -> planner -> gate/up+SwiGLU -> down -> combine, where
+for few tokens the router runs inside the planner and, for bf16 weights, both
+inside the gate/up launch (the header's launch count tells which).  No
 host synchronisation, no allocation and no host readback happen in ``run()``;
 the prepared object owns its output and workspace, binds the caller's tensors
 by address, and may be captured in a HIP graph.  Values of the bound inputs
@@ -161,8 +163,11 @@ class PreparedMoE:
         self.num_tasks = view(lay.num_tasks, 1)
         self.activated = view(lay.act, r * inter, torch.bfloat16).view(r, inter)
         self.routed_output = view(lay.routed, r * h, torch.bfloat16).view(r, h)
-        names = (["router"] if (logits is not None and lay.launches == 5) else []) + \
-            ["route_plan", "gate_up_swiglu", "down", "combine"]
+        if lay.launches == 3:  # gate/up routes and plans in its prologue
+            names = ["gate_up_swiglu", "down", "combine"]
+        else:
+            names = (["router"] if (logits is not None and lay.launches == 5) else []) + \
+                ["route_plan", "gate_up_swiglu", "down", "combine"]
         self.launches = tuple(names) if t else ()
         self.fast_path = bool(lay.fast_path)
 

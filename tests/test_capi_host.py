@@ -77,10 +77,14 @@ def test_layout_for_qwen_shape():
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=193))
     assert lay.launches == 5
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16))
-    assert lay.launches == 4
+    assert lay.launches == 3
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17))
-    assert lay.launches == 4  # two tokens per planner wave (E <= 128)
+    assert lay.launches == 3  # bf16: routing and planning in the gate/up launch
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=32))
+    assert lay.launches == 3
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, fmt=N.WEIGHTS_W4G128))
+    assert lay.launches == 4  # W4: router fused into the planner
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, H=4096))
     assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=33))
     assert lay.launches == 5

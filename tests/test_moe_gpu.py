@@ -345,3 +345,33 @@ def test_fused_router_two_tokens_per_wave(tokens, experts, k, gpu_device):
     plan.logits[tokens - 1, experts // 2] = float("nan")
     plan.forward()
     assert plan.read_status() & 4
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 16, 17, 31, 32])
+def test_gate_up_with_planning_prologue(tokens, gpu_device):
+    """bf16 Qwen shape, T <= 32: the gate/up launch routes and plans in its
+    prologue (no planner launch).  IDs bit-exact on tie-heavy logits, weights to
+    fp32 rounding, every global plan array equal to the canonical dispatch,
+    the layer within tolerance and bitwise equal to the fixed-route path on the
+    same routes; a NaN logit raises status bit 2."""
+    lay = make_layer("qwen", tokens, seed=tokens, device=gpu_device)
+    g = torch.Generator().manual_seed(tokens)
+    logits = (torch.randint(-6, 6, (tokens, lay["E"]), generator=g).float() * 0.75).to(gpu_device)
+    plan = prepare_routed_moe(lay["x"], logits, lay["gate_up"], lay["down"], 8)
+    assert plan.launches == ("gate_up_swiglu", "down", "combine")
+    out = plan.forward().clone()
+    torch.cuda.synchronize()
+    ids, w = O.route_topk(logits.cpu(), 8)
+    assert torch.equal(plan.ids.cpu(), ids), "router IDs differ"
+    assert torch.allclose(plan.routing_weights.cpu(), w, rtol=2e-6, atol=1e-7)
+    _check_dispatch(plan, ids, lay["E"])
+    assert plan.read_status() == 0
+    x, gu, dn = lay["x"].cpu(), lay["gate_up"].cpu(), lay["down"].cpu()
+    m = O.error(out, O.moe_reference(x, gu, dn, ids, w))
+    assert m["passed"], m
+    fixed = prepare_moe(lay["x"], lay["gate_up"], lay["down"], plan.ids.clone(),
+                        plan.routing_weights.clone())
+    assert torch.equal(fixed.run().view(torch.int16), out.view(torch.int16))
+    logits[tokens - 1, 5] = float("nan")
+    plan.forward()
+    assert plan.read_status() & 4
