@@ -92,7 +92,10 @@ typedef struct moe_layout {
   size_t total;       /* workspace bytes                                          */
   int32_t task_capacity;
   int32_t token_block;
-  int32_t launches;   /* kernel launches per forward (0 when T == 0)             */
+  int32_t launches;   /* kernel launches per forward: 5 router, plan, gate/up,   *
+                       * down, combine; 4 with the router fused into the planner *
+                       * or fixed routes; 3 when the bf16 gate/up launch routes  *
+                       * and plans itself (T <= 32); 0 when T == 0               */
   int32_t fast_path;  /* 0 generic kernels (unaligned shapes), 1 MFMA weight      
                          streaming, 2 MFMA LDS-tiled (many rows per expert)     */
 } moe_layout;
