@@ -289,11 +289,14 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     }
   };
 
-  auto epilogue = [&](const Meta &m, int parity) {
+  auto epilogue = [&](const Meta &m, int parity, int rot) {
     const f32x4 *red = s_red + (size_t)parity * kConsumers * NRB * MT * kWave;
     if (KIND == 0) {
-      if (tid < MT * 4 * kWave) {
-        const int l = tid & 63, i = (tid >> 6) & 3, mt = tid >> 8;
+      // The threads of the epilogue rotate over the MFMA waves from unit to unit.
+      constexpr int EN = MT * 4 * kWave;
+      const int et = tid - (rot % (kConsumers * kWave / EN)) * EN;
+      if (et >= 0 && et < EN) {
+        const int l = et & 63, i = (et >> 6) & 3, mt = et >> 8;
         const int j = mt * 16 + (l & 15);
         const float *redf = (const float *)red;
         auto part = [&](int w, int rb) { return redf[(((w * NRB + rb) * MT + mt) * kWave + l) * 4 + i]; };
@@ -311,9 +314,11 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
               (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
       }
     } else {
-      if (tid < NRB * MT * kWave) {
-        const int rb = tid / (MT * kWave);
-        const int mt = (tid >> 6) % MT, l = tid & 63;
+      constexpr int EN = NRB * MT * kWave;
+      const int et = tid - (rot % (kConsumers * kWave / EN)) * EN;
+      if (et >= 0 && et < EN) {
+        const int rb = et / (MT * kWave);
+        const int mt = (et >> 6) % MT, l = et & 63;
         const int j = mt * 16 + (l & 15);
         f32x4 sm = red[(rb * MT + mt) * kWave + l];
 #pragma unroll
@@ -347,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
 #pragma unroll
     for (int s = 0; s < SPU; ++s, ++st) {
       lds_barrier();  // stage st published; unit i-1's partials published
-      if (s == 0 && i > 0) epilogue(prev, (i - 1) % C::PAR);
+      if (s == 0 && i > 0) epilogue(prev, (i - 1) % C::PAR, (i - 1) & 1);
       const uint8_t *buf = smem + (st % NS) * C::STAGE;
       u32x4 af[KKS][NRB];
 #pragma unroll
@@ -374,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     prev = cur;
   }
   lds_barrier();
-  epilogue(prev, (count - 1) % C::PAR);
+  epilogue(prev, (count - 1) % C::PAR, (count - 1) & 1);
 }
 
 template <int KIND, int MT, int SPU, bool PLAN = false>

@@ -239,11 +239,14 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
     if (KIND == 0) {
       // One output per thread (4 waves per token block), so no single wave
       // carries the epilogue's latency into the next unit's barrier.
-      if (tid < MT * 4 * kWave) {
-        const int l = tid & 63, i = (tid >> 6) & 3, mt = tid >> 8;
+      // The threads of the epilogue rotate over the waves from unit to unit.
+      constexpr int EN = MT * 4 * kWave;
+      const int et = tid - ((i & 1) % (kThreads / EN)) * EN;
+      if (et >= 0 && et < EN) {
+        const int l = et & 63, ii = (et >> 6) & 3, mt = et >> 8;
         const int j = mt * 16 + (l & 15);
         const float *redf = (const float *)red;
-        auto part = [&](int w, int rb) { return redf[(((w * NRB + rb) * MT + mt) * kWave + l) * 4 + i]; };
+        auto part = [&](int w, int rb) { return redf[(((w * NRB + rb) * MT + mt) * kWave + l) * 4 + ii]; };
         float sg = part(0, 0), su = part(0, 1);
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) {
@@ -254,13 +257,15 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
         const float up = bf16_round(su);
         const float v = gt / (1.0f + expf(-gt)) * up;
         if (j < cur.rows)
-          a.act[(size_t)(cur.row0 + j) * I + cur.cb * 16 + 4 * (l >> 4) + i] =
+          a.act[(size_t)(cur.row0 + j) * I + cur.cb * 16 + 4 * (l >> 4) + ii] =
               (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
       }
     } else {
-      if (tid < NRB * MT * kWave) {
-        const int rb = tid / (MT * kWave);
-        const int mt = (tid >> 6) % MT, l = tid & 63;
+      constexpr int EN = NRB * MT * kWave;
+      const int et = tid - ((i & 1) % (kThreads / EN)) * EN;
+      if (et >= 0 && et < EN) {
+        const int rb = et / (MT * kWave);
+        const int mt = (et >> 6) % MT, l = et & 63;
         const int j = mt * 16 + (l & 15);
         f32x4 sm = red[(rb * MT + mt) * kWave + l];
 #pragma unroll
