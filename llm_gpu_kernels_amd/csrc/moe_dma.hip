@@ -4,11 +4,11 @@
 // cuda_gate_up_bf16, cuda_gate_up.cu:53-131) and the down projection
 // (_dynamic_grouped, moe.py:69-95).
 //
-// Same units as the register-streaming kernel -- (task, 16 act columns) with
-// 16 gate + 16 up weight rows, or (task, 32 hidden columns) -- and the same
-// split-K over eight MFMA waves with a fixed-order reduction, but the weights
-// reach the matrix cores through LDS:
-//  * eight loader waves move each unit's 32 weight rows in K-stages of KC
+// Units like the register-streaming kernel's -- (task, 16 act columns) with
+// 16 gate + 16 up weight rows, or (task, 64 hidden columns) of down -- and
+// the same split-K over eight MFMA waves with a fixed-order reduction, but the
+// weights reach the matrix cores through LDS:
+//  * eight loader waves move each unit's 32 (64) weight rows in K-stages of KC
 //    elements with gfx950's 16-byte global -> LDS loads; every load
 //    instruction reads one contiguous 1 KiB piece (one row's KC = 512
 //    elements, or two rows' 256), the pattern HBM streams fastest (6.5 TB/s
@@ -21,7 +21,8 @@
 //    bank-conflict free) against token rows held in registers for the whole
 //    task (reloaded only on a task switch, on the MFMA waves' own counter);
 //  * a unit's eight partial tiles are written to LDS after its last stage and
-//    reduced, in fixed wave order, after the next stage barrier.
+//    reduced, in fixed wave order, after the next stage barrier (by threads
+//    of alternating waves from unit to unit).
 // One 1024-thread workgroup per CU; persistent workgroups take blocks of
 // consecutive units.  Rounding as in moe_stream.hip.
 #include "common.h"
@@ -35,9 +36,13 @@ namespace moe {
 namespace {
 
 constexpr int kConsumers = 8;
+constexpr int kDownRows = 64;
 constexpr int kLoaders = 8;
 constexpr int kThreads = (kConsumers + kLoaders) * kWave;
-constexpr int kRows = 32;  // weight rows per unit
+// Weight rows per unit: gate/up 16 gate + 16 up rows; down 64 rows (measured
+// 0.3-1 us faster than 32-row units at T = 17 and 193).
+template <int KIND>
+constexpr int kRowsOf = KIND == 1 ? kDownRows : 32;
 constexpr int kWaitVmcntZero = (7 << 4) | (15 << 8);
 
 template <typename T>
@@ -73,15 +78,18 @@ constexpr int kPlanBytes = kPlanTaskMax * 16 + (route_dev::kSmallPlanRoutes + 64
 
 template <int KIND, int MT, bool PLAN = false>
 struct DmaCfg {
+  static constexpr int ROWS = kRowsOf<KIND>;
+  static constexpr int NRB = ROWS / 16;                   // 16-row MFMA blocks per unit
   static constexpr int KC = KIND == 0 ? 512 : 256;      // K per stage
-  static constexpr int STAGE = kRows * KC * 2;            // bytes
+  static constexpr int STAGE = ROWS * KC * 2;             // bytes
   static constexpr int KKS = KC / kConsumers / 32;        // k-steps per wave per stage
-  // Partial tiles: two buffers by unit parity; one suffices with two or more
-  // stages per unit (always so for PLAN): the next unit writes its partials
-  // only after its second stage barrier, which every wave reaches after its
-  // part of the reduction.
-  static constexpr int PAR = PLAN ? 1 : 2;
-  static constexpr int RED = PAR * kConsumers * 2 * MT * kWave * 16;
+  // Partial tiles of one unit, reduced after the first stage barrier of the
+  // next unit.  One buffer suffices because every unit has two or more
+  // stages (checked in the kernel): the next unit writes its partials only
+  // after its second stage barrier, which every wave reaches after its part
+  // of the reduction.
+  static constexpr int PAR = 1;
+  static constexpr int RED = PAR * kConsumers * NRB * MT * kWave * 16;
   static constexpr int PLANB = PLAN ? kPlanBytes : 0;
   static constexpr int NS0 = (int)((kMaxLds - RED - PLANB) / STAGE);
   // Ring depth: down's 16 KiB stages stream best with four ahead (measured:
@@ -107,9 +115,10 @@ __device__ __forceinline__ int stage_off(int R, int c) {
 template <int KIND, int MT, int SPU, bool PLAN = false>
 __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs ra) {
   using C = DmaCfg<KIND, MT, PLAN>;
-  static_assert(!PLAN || (KIND == 0 && MT == 1 && SPU >= 2), "planning prologue: 16-row gate/up");
+  static_assert(!PLAN || (KIND == 0 && MT == 1), "planning prologue: 16-row gate/up");
+  static_assert(SPU >= 2, "one partial buffer needs two or more stages per unit");
   constexpr int KC = C::KC, KKS = C::KKS, NS = C::NS, PER = C::PER;
-  constexpr int NRB = 2;
+  constexpr int NRB = C::NRB, ROWS = C::ROWS;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   f32x4 *s_red = (f32x4 *)(smem + NS * C::STAGE);  // [2][kConsumers][NRB][MT][64]
 
@@ -118,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   const int lane = tid & (kWave - 1);
   const int H = a.H, I = a.I;
   const int K = KIND == 0 ? H : I;  // == SPU * KC (checked on the host)
-  const int ncb = KIND == 0 ? I / 16 : H / 32;  // units per task
+  const int ncb = KIND == 0 ? I / 16 : H / ROWS;  // units per task
   const int4 *l_tasks = nullptr;
   const int *l_row_token = nullptr;
   int ntasks = 0;
@@ -206,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         const int R = (lw * PER + j) * RPI + lrow;  // stage row
         size_t grow;
         if (KIND == 0) grow = (size_t)e * 2 * I + (R < 16 ? cb * 16 + R : I + cb * 16 + R - 16);
-        else grow = (size_t)e * H + cb * 32 + R;
+        else grow = (size_t)e * H + cb * ROWS + R;
         const int c = lch ^ (R & 15);  // the chunk that belongs at LDS chunk lch
         src[j] = (KIND == 0 ? a.gate_up : a.down) + grow * K + c * 8;
       }
@@ -328,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         packed[0] = pack_bf16x2(sm[0], sm[1]);
         packed[1] = pack_bf16x2(sm[2], sm[3]);
         if (j < m.rows)
-          *(u32x2 *)(a.routed + (size_t)q * H + m.cb * 32 + rb * 16 + 4 * (l >> 4)) = packed;
+          *(u32x2 *)(a.routed + (size_t)q * H + m.cb * ROWS + rb * 16 + 4 * (l >> 4)) = packed;
       }
     }
   };
