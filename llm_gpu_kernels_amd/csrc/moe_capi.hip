@@ -135,7 +135,7 @@ moe_layout compute_layout(const moe_desc *d) {
   L.row_token = take(R * 4 + 64 * 4);
   L.tasks = take(cap * 16);
   L.num_tasks = take(4);
-  L.counters = take(2 * 4);
+  L.counters = take(4 * 4);
   L.act = take(R * (size_t)d->I * 2);
   L.routed = take(R * (size_t)d->H * 2);
   L.total = o;
@@ -228,6 +228,12 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
   if (e != hipSuccess) {
     delete p;
     return hip_fail(e, "device query");
+  }
+  // The streaming GEMMs' work counters start at zero; every launch leaves
+  // them at zero.
+  if (d->T > 0 && (e = hipMemset((char *)d->workspace + L.counters, 0, 4 * sizeof(int32_t))) != hipSuccess) {
+    delete p;
+    return hip_fail(e, "zeroing the work counters");
   }
   *out = p;
   return MOE_OK;

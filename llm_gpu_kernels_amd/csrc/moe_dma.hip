@@ -39,10 +39,10 @@ constexpr int kConsumers = 8;
 constexpr int kDownRows = 64;
 constexpr int kLoaders = 8;
 constexpr int kThreads = (kConsumers + kLoaders) * kWave;
-// Weight rows per unit: gate/up 16 gate + 16 up rows; down 64 rows (measured
-// 0.3-1 us faster than 32-row units at T = 17 and 193).
-template <int KIND>
-constexpr int kRowsOf = KIND == 1 ? kDownRows : 32;
+// Weight rows per unit: gate/up 16 gate + 16 up rows; down kDownRows rows
+// with 16-row tasks, 32 with 32-row tasks (whose partials take twice the LDS).
+template <int KIND, int MT>
+constexpr int kRowsOf = KIND == 1 && MT == 1 ? kDownRows : 32;
 constexpr int kWaitVmcntZero = (7 << 4) | (15 << 8);
 
 template <typename T>
@@ -76,9 +76,31 @@ __device__ __forceinline__ void wait_vmcnt() {
 constexpr int kPlanTaskMax = route_dev::kMaxExperts + route_dev::kSmallPlanRoutes / 16;
 constexpr int kPlanBytes = kPlanTaskMax * 16 + (route_dev::kSmallPlanRoutes + 64) * 4 + 16;
 
+// Work distribution.  Workgroup b first takes units A b .. A b + A - 1; every
+// later unit comes from a device-wide counter, kChunk consecutive units per
+// atomic add, so a workgroup that streams faster takes more units (static
+// blocks of equal size measured a 20 us spread of finish times at T = 17, and
+// T = 193 gate/up 145 -> 135 us with the counter).  MFMA wave 0 takes the
+// unit A units ahead of the one it starts, and publishes it one unit later in
+// an LDS ring that the loaders read when they set that unit up.  The counter
+// pair {units handed out, workgroups finished} is reset by the last
+// workgroup to finish, so it is zero at every launch.
+constexpr int kSeqRing = 8;
+// Units per counter step: pairs of consecutive units (fewer task switches)
+// measured 2-8 us faster per launch than single units at T = 17 and 193, and
+// than larger blocks, which leave longer tails.
+constexpr int kChunk = 2;
+
+__device__ __forceinline__ void finish_units(int32_t *w, int G) {
+  if (atomicAdd(w + 1, 1) == G - 1) {
+    atomicExch(w, 0);
+    atomicExch(w + 1, 0);
+  }
+}
+
 template <int KIND, int MT, bool PLAN = false>
 struct DmaCfg {
-  static constexpr int ROWS = kRowsOf<KIND>;
+  static constexpr int ROWS = kRowsOf<KIND, MT>;
   static constexpr int NRB = ROWS / 16;                   // 16-row MFMA blocks per unit
   static constexpr int KC = KIND == 0 ? 512 : 256;      // K per stage
   static constexpr int STAGE = ROWS * KC * 2;             // bytes
@@ -91,15 +113,27 @@ struct DmaCfg {
   static constexpr int PAR = 1;
   static constexpr int RED = PAR * kConsumers * NRB * MT * kWave * 16;
   static constexpr int PLANB = PLAN ? kPlanBytes : 0;
-  static constexpr int NS0 = (int)((kMaxLds - RED - PLANB) / STAGE);
-  // Ring depth: down's 16 KiB stages stream best with four ahead (measured:
-  // 0.5 us faster than seven ahead at T = 17 and 193); gate/up keeps all it fits.
+  static constexpr int SEQB = kSeqRing * 4;
+  static constexpr int NS0 = (int)((kMaxLds - RED - PLANB - SEQB) / STAGE);
+  // Ring depth: at most five stages for down (with 16 KiB stages, four ahead
+  // measured 0.5 us faster than seven); its 64-row units' 32 KiB stages fit
+  // three beside the partials and the unit ring.  Gate/up keeps all it fits.
   static constexpr int NSMAX = KIND == 1 ? 5 : 8;
   static constexpr int NS = NS0 > NSMAX ? NSMAX : NS0;
   static constexpr int PER = STAGE / 1024 / kLoaders;     // 1 KiB loads per stage per loader
   static_assert(NS >= 3, "at least two stages ahead");
   static_assert((NS - 2) * PER < 64, "vmcnt range");
+  static constexpr int LDS = NS * STAGE + RED + PLANB + SEQB;
 };
+
+// Units taken ahead: a unit taken at the start of unit k is published at the
+// start of unit k + 1 and must be visible (one barrier later) when the
+// loaders set up its first stage, NS - 1 stages ahead of the MFMA waves:
+// (A - 1) SPU >= NS.  A is also how many units a workgroup holds when the
+// counter runs out, so it is kept at that minimum (one more unit ahead
+// measured 10 us slower at T = 17).
+template <int NS, int SPU>
+constexpr int kAheadOf = 1 + (NS + SPU - 1) / SPU;
 
 // Byte offset in a stage of 16-byte chunk c of stage row R (rows of KC elements).
 template <int KC>
@@ -133,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   int ntasks = 0;
   if constexpr (PLAN) {
     using namespace route_dev;
-    uint8_t *pa = smem + NS * C::STAGE + C::RED;
+    uint8_t *pa = smem + NS * C::STAGE + C::RED + C::SEQB;
     int4 *p_tasks = (int4 *)pa;
     int *p_row = (int *)(pa + kPlanTaskMax * 16);
     int *p_nt = p_row + kSmallPlanRoutes + 64;
@@ -175,11 +209,19 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   }
   const int total = (PLAN ? ntasks : *as_const(a.num_tasks)) * ncb;
   const int G = gridDim.x;
-  const int cper = (total + G - 1) / G;
-  const int b0 = (int)blockIdx.x * cper;
-  const int count = b0 < total ? min(cper, total - b0) : 0;
-  if (count <= 0) return;
-  const int nstages = count * SPU;
+  constexpr int A = kAheadOf<NS, SPU>;
+  static_assert(A + 1 <= kSeqRing, "unit ring");
+  int32_t *const wcnt = a.counters + 2 * KIND;
+  int *const seq = (int *)(smem + NS * C::STAGE + C::RED);
+  // Units taken without the counter: S consecutive ones per workgroup.
+  // (Static shares up to 7/8 of the work, the rest from the counter,
+  // measured slower: the per-workgroup streaming rate varies too much.)
+  constexpr int S = A;
+  const int ub = (int)blockIdx.x * S;  // this workgroup's first unit
+  if (ub >= total) {
+    if (tid == 0) finish_units(wcnt, G);
+    return;
+  }
   const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
 
   if (wave >= kConsumers) {
@@ -207,9 +249,8 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         return tasks[4 * t];
       }
     };
-    auto setup = [&](int u) {
+    auto setup = [&](int u, int e) {
       const int t = u / ncb, cb = u - t * ncb;
-      const int e = expert_of(t);
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         const int R = (lw * PER + j) * RPI + lrow;  // stage row
@@ -220,10 +261,30 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         src[j] = (KIND == 0 ? a.gate_up : a.down) + grow * K + c * 8;
       }
     };
-    auto issue = [&](int st) {
+    // Unit k of this workgroup (k >= A: published by MFMA wave 0, read
+    // through an instruction the compiler cannot see).
+    auto unit_at = [&](int k) -> int {
+      if (k < S) return ub + k;
+      uint32_t v;
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                   : "=v"(v)
+                   : "v"((uint32_t)(size_t)(const __attribute__((address_space(3))) int *)(seq + k % kSeqRing))
+                   : "memory");
+      return __builtin_amdgcn_readfirstlane(v);
+    };
+    int issued = 0;
+    bool ended = false;
+    // Issues stage `issued` unless its unit is past the end.
+    auto issue = [&]() {
+      const int st = issued;
       const int i = st / SPU, s = st - (st / SPU) * SPU;
       if (i != cur) {
-        setup(b0 + i);
+        const int u = unit_at(i);
+        if (u >= total) {
+          ended = true;
+          return;
+        }
+        setup(u, expert_of(u / ncb));
         cur = i;
       }
       uint8_t *buf = smem + (st % NS) * C::STAGE;
@@ -232,11 +293,12 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         __builtin_amdgcn_global_load_lds(
             (const void *)(src[j] + s * KC),
             (__attribute__((address_space(3))) void *)(buf + (lw * PER + j) * 1024), 16, 0, 0);
+      ++issued;
     };
-    for (int st = 0; st < NS - 1 && st < nstages; ++st) issue(st);
-    for (int st = 0; st < nstages; ++st) {
+    while (issued < NS - 1 && !ended) issue();
+    for (int st = 0; st < issued; ++st) {
       // Stage st has landed once at most the loads issued after it remain.
-      const int later = min(NS - 2, nstages - 1 - st);
+      const int later = issued - 1 - st;
       switch (later) {
         case 0: wait_vmcnt<0>(); break;
         case 1: wait_vmcnt<PER>(); break;
@@ -248,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
       }
       loader_barrier();
       // Buffer (st - 1) % NS was last read before this barrier.
-      if (st + NS - 1 < nstages) issue(st + NS - 1);
+      if (!ended) issue();
     }
     loader_barrier();  // the MFMA waves' last reduction barrier
     return;
@@ -279,22 +341,27 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   };
 
   // Token rows of the task: fragment [mt][s * KKS + kk] = row mt*16 + r,
-  // K = s*KC + wave*KC/8 + kk*32 + 8g .. +8.  Rows past the task's end read
-  // row 0 (finite data in columns the epilogue never stores).
-  u32x4 bfr[MT][SPU * KKS];
-  auto load_b = [&](const Meta &m) {
+  // K = s*KC + wave*KC/8 + kk*32 + 8g .. +8.  Rows past the task's end are
+  // zero (columns the epilogue never stores).
+  // The next task's rows load behind the current unit's MFMAs when a second
+  // set fits in registers (else at the switch, with a wait).
+  constexpr bool PREF = MT * SPU * KKS * 4 <= 32;
+  u32x4 bfr[MT][SPU * KKS], bnext[MT][SPU * KKS];
+  auto load_b = [&](const Meta &m, u32x4(&dst)[MT][SPU * KKS]) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int j = mt * 16 + r;
       const bool ok = j < m.rows;
+      const int q = __shfl(m.idxv, j, kWave);
       size_t row;
-      if (KIND == 0) row = (size_t)(ok ? __shfl(m.idxv, j, kWave) : 0) * H;
-      else row = (size_t)(ok ? m.row0 + j : 0) * I;
+      if (KIND == 0) row = (size_t)q * H;
+      else row = (size_t)(m.row0 + j) * I;
       const uint16_t *b = (KIND == 0 ? a.x : a.act) + row + wave * (KC / 8) + g * 8;
 #pragma unroll
       for (int s = 0; s < SPU; ++s)
 #pragma unroll
-        for (int kk = 0; kk < KKS; ++kk) bfr[mt][s * KKS + kk] = *(const u32x4 *)(b + s * KC + kk * 32);
+        for (int kk = 0; kk < KKS; ++kk)
+          dst[mt][s * KKS + kk] = ok ? *(const u32x4 *)(b + s * KC + kk * 32) : u32x4{0u, 0u, 0u, 0u};
     }
   };
 
@@ -342,17 +409,17 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     }
   };
 
-  Meta prev;
-  prev.task = -1;
-  int btask = -1;
+  // Unit k of this workgroup, k >= A: published by MFMA wave 0 at the start
+  // of unit k - A + 1 (visible to every wave one barrier later).
+  auto unit_at = [&](int k) -> int { return k < S ? ub + k : seq[k % kSeqRing]; };
+  Meta prev, cur = meta_of(ub), next;
+  load_b(cur, bfr);
+  int taken = 0;       // wave 0, lane 0: counter value of the unit taken last
+  bool taking = true;  // wave 0: the units taken so far are all in range
+  bool pending = false;
   int st = 0;
-  for (int i = 0; i < count; ++i) {
-    const Meta cur = meta_of(b0 + i);
-    if (cur.task != btask) {
-      load_b(cur);
-      __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
-      btask = cur.task;
-    }
+  for (int i = 0;; ++i) {
+    int un = total;  // unit i + 1
     f32x4 acc[NRB][MT];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb)
@@ -361,7 +428,30 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
 #pragma unroll
     for (int s = 0; s < SPU; ++s, ++st) {
       lds_barrier();  // stage st published; unit i-1's partials published
-      if (s == 0 && i > 0) epilogue(prev, (i - 1) % C::PAR, (i - 1) & 1);
+      if (s == 0) {
+        if (i > 0) epilogue(prev, (i - 1) % C::PAR, (i - 1) & 1);
+        if (wave == 0) {
+          if (pending) {  // unit i - 1 + A, taken at the start of unit i - 1
+            const int u = __builtin_amdgcn_readfirstlane(taken) + S * G;
+            if (lane == 0) seq[(i - 1 + A) % kSeqRing] = u;
+            taking = u < total;
+            pending = false;
+          }
+          if (taking) {  // unit i + A
+            if (lane == 0) taken = (i % kChunk) ? taken + 1 : kChunk * atomicAdd(wcnt, 1);
+            pending = true;
+          }
+        }
+      }
+      if (s == 1) {
+        // The next unit; its token rows load behind this unit's MFMAs when
+        // it belongs to another task.
+        un = unit_at(i + 1);
+        if (un < total) {
+          next = meta_of(un);
+          if (PREF && next.task != cur.task) load_b(next, bnext);
+        }
+      }
       const uint8_t *buf = smem + (st % NS) * C::STAGE;
       u32x4 af[KKS][NRB];
 #pragma unroll
@@ -386,16 +476,36 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) red[((wave * NRB + rb) * MT + mt) * kWave + lane] = acc[rb][mt];
     prev = cur;
+    if (un >= total) {
+      lds_barrier();
+      epilogue(prev, i % C::PAR, i & 1);
+      break;
+    }
+    if (next.task != cur.task) {
+      if constexpr (PREF) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < SPU * KKS; ++j) bfr[mt][j] = bnext[mt][j];
+      } else {
+        load_b(next, bfr);
+      }
+    }
+    cur = next;
   }
-  lds_barrier();
-  epilogue(prev, (count - 1) % C::PAR, (count - 1) & 1);
+  // Every unit this workgroup took has been read back (or is waited for
+  // here) before it counts itself finished.
+  if (wave == 0) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+    if (lane == 0) finish_units(wcnt, G);
+  }
 }
 
 template <int KIND, int MT, int SPU, bool PLAN = false>
 hipError_t launch_one(const ExpertArgs &a, int num_cus, hipStream_t s, const RouteArgs *ra = nullptr) {
   using C = DmaCfg<KIND, MT, PLAN>;
   auto k = dma_kernel<KIND, MT, SPU, PLAN>;
-  const size_t lds = (size_t)C::NS * C::STAGE + C::RED + C::PLANB;
+  const size_t lds = C::LDS;
   static const bool attr = hipFuncSetAttribute((const void *)k,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds) == hipSuccess;

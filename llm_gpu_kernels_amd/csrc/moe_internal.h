@@ -16,7 +16,7 @@ struct RouteArgs {
   int32_t *row_token;      // [R] token of grouped row p (row_route[p] / K)
   int4 *tasks;             // {expert, first grouped row, rows, 0}
   int32_t *num_tasks;
-  int32_t *counters;       // [2] work counters of the streaming GEMMs (zeroed here)
+  int32_t *counters;       // [4] work counters of the streaming GEMMs
   int T, K, E, R;
   int route_logits, renormalize, id64, fuse_router;
   int token_block;
@@ -32,7 +32,7 @@ struct ExpertArgs {
   const float *weights;        // [T, K]
   const int32_t *map, *row_route, *row_token, *num_tasks;
   const int4 *tasks;
-  int32_t *counters;           // [2] work counters (gate/up, down)
+  int32_t *counters;           // [4] {units taken, workgroups done} of gate/up, down
   uint16_t *act;               // [R, I] bf16, grouped-row order
   uint16_t *routed;            // [R, H] bf16, route order
   uint16_t *out;               // [T, H] bf16

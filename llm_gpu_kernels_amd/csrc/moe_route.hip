@@ -296,8 +296,6 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   if (tid == 0) {
     *a.num_tasks = sh.toff[E];
     a.status[0] = sh.status;
-    a.counters[0] = 0;
-    a.counters[1] = 0;
   }
 }
 
