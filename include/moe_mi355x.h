@@ -86,7 +86,7 @@ typedef struct moe_layout {
   size_t row_token;   /* [R]  token of grouped row p (row_route[p] / K)          */
   size_t tasks;       /* [task_capacity][4] {expert, first row, rows, 0}         */
   size_t num_tasks;   /* [1]                                                     */
-  size_t counters;    /* [2]  work counters of the streaming GEMMs               */
+  size_t counters;    /* [4]  work counters of the streaming GEMMs (0 between launches) */
   size_t act;         /* [R, I] bf16 SwiGLU activations in grouped-row order     */
   size_t routed;      /* [R, H] bf16 down projections in route order             */
   size_t total;       /* workspace bytes                                          */

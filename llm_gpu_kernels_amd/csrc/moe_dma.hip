@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     __syncthreads();
     const SmallPlanLds L{x_ids, x_w, x_wcnt, x_cnt, x_off, x_toff, p_tasks, p_row, p_nt, x_flags};
     const SmallPlanOut O{ra.counts, ra.offsets, ra.ranks, ra.map, ra.row_route, ra.row_token,
-                         ra.tasks, ra.num_tasks, ra.counters, ra.status};
+                         ra.tasks, ra.num_tasks, ra.status};
     plan_small(L, O, g0, ra.R, ra.E, ra.K, 16, flags);
     ntasks = *p_nt;
     l_tasks = p_tasks;

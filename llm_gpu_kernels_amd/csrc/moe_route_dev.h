@@ -195,7 +195,7 @@ struct SmallPlanLds {
 struct SmallPlanOut {
   int32_t *counts, *offsets, *ranks, *map, *row_route, *row_token;
   int4 *tasks;
-  int32_t *num_tasks, *counters;
+  int32_t *num_tasks;
   uint32_t *status;
 };
 
@@ -300,8 +300,6 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
   if (g && tid == 0) {
     *g->num_tasks = s.toff[E];
     g->status[0] = *s.flags;
-    g->counters[0] = 0;
-    g->counters[1] = 0;
   }
 }
 

@@ -161,6 +161,9 @@ class PreparedMoE:
         self.row_route = view(lay.row_route, r)
         self.tasks = view(lay.tasks, 4 * lay.task_capacity).view(-1, 4)
         self.num_tasks = view(lay.num_tasks, 1)
+        # {units taken, workgroups finished} of the gate/up and down launches
+        # that hand out work from a device counter; zero between launches.
+        self.work_counters = view(lay.counters, 4)
         self.activated = view(lay.act, r * inter, torch.bfloat16).view(r, inter)
         self.routed_output = view(lay.routed, r * h, torch.bfloat16).view(r, h)
         if lay.launches == 3:  # gate/up routes and plans in its prologue

@@ -347,6 +347,30 @@ def test_fused_router_two_tokens_per_wave(tokens, experts, k, gpu_device):
     assert plan.read_status() & 4
 
 
+@pytest.mark.parametrize("tokens", [17, 193])
+def test_work_counters_return_to_zero(tokens, gpu_device):
+    """Qwen shape, bf16: the LDS-streaming gate/up and down launches hand out
+    units from device-wide counters that the last workgroup of each launch
+    resets.  After every forward the counters read zero, and forwards over
+    new tokens (T = 17: routed in the gate/up prologue; T = 193: planner
+    launch) each match the oracle -- a unit skipped or taken twice by a
+    stale counter would leave the previous forward's rows in the output."""
+    lay = make_layer("qwen", tokens, seed=50 + tokens, device=gpu_device)
+    g = torch.Generator().manual_seed(tokens)
+    logits = torch.randn(tokens, lay["E"], generator=g).to(gpu_device)
+    plan = prepare_routed_moe(lay["x"], logits, lay["gate_up"], lay["down"], 8)
+    gu, dn = lay["gate_up"].cpu(), lay["down"].cpu()
+    for it in range(3 if tokens <= 32 else 2):
+        lay["x"].copy_((torch.randn(lay["x"].shape, generator=g) * 0.5).to(torch.bfloat16))
+        logits.copy_(torch.randn(tokens, lay["E"], generator=g))
+        out = plan.forward().clone()
+        torch.cuda.synchronize()
+        assert plan.work_counters.cpu().tolist() == [0, 0, 0, 0], it
+        m = O.error(out, O.moe_reference(lay["x"].cpu(), gu, dn, plan.ids.cpu(),
+                                         plan.routing_weights.cpu()))
+        assert m["passed"], (it, m)
+
+
 @pytest.mark.parametrize("tokens", [1, 2, 16, 17, 31, 32])
 def test_gate_up_with_planning_prologue(tokens, gpu_device):
     """bf16 Qwen shape, T <= 32: the gate/up launch routes and plans in its
