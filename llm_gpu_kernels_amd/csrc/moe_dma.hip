@@ -19,12 +19,14 @@
 //  * the MFMA waves read their K-slice of a stage as MFMA A fragments
 //    (16-byte chunks XOR-swizzled by row on the global side, so the reads are
 //    bank-conflict free) against token rows held in registers for the whole
-//    task (reloaded only on a task switch, on the MFMA waves' own counter);
+//    task (the next task's rows load during the unit before the switch);
 //  * a unit's eight partial tiles are written to LDS after its last stage and
 //    reduced, in fixed wave order, after the next stage barrier (by threads
 //    of alternating waves from unit to unit).
-// One 1024-thread workgroup per CU; persistent workgroups take blocks of
-// consecutive units.  Rounding as in moe_stream.hip.
+// One 1024-thread workgroup per CU; persistent workgroups take their units
+// from a device-wide counter (below), and the MFMA waves load the next
+// task's token rows behind the current unit's MFMAs.  Rounding as in
+// moe_stream.hip.
 #include "common.h"
 #include "moe_internal.h"
 #include "moe_route_dev.h"
