@@ -65,6 +65,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   const int wave = tid >> 6;
   const int lane = tid & (kWave - 1);
   const int E = a.E;
+  const int nbits = id_bits(E);
   // Fused router: one token per wave (mode 1, T <= 16) or per half-wave
   // (mode 2, T <= 32, E <= 128); the logits are requested before the set-up.
   const int fmode = LDSR && a.route_logits ? a.fuse_router : 0;
@@ -126,6 +127,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
     uint64_t match = __ballot(ok);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {
+      if (bit >= nbits) break;  // every id is below 2^nbits
       const bool set = (id >> bit) & 1;
       const uint64_t b = __ballot(ok && set);
       match &= set ? b : ~b;
@@ -186,6 +188,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
       uint64_t match = __ballot(ok);
 #pragma unroll
       for (int bit = 0; bit < 8; ++bit) {
+        if (bit >= nbits) break;
         const bool set = (id >> bit) & 1;
         const uint64_t bb = __ballot(ok && set);
         match &= set ? bb : ~bb;

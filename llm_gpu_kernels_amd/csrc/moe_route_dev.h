@@ -199,6 +199,9 @@ struct SmallPlanOut {
   uint32_t *status;
 };
 
+// Bits of an expert id below E (E <= 256).
+__device__ __forceinline__ int id_bits(int E) { return E <= 1 ? 1 : 32 - __builtin_clz((unsigned)(E - 1)); }
+
 // Called by all 1024 threads after the routes are visible in LDS.
 __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go, bool write_global,
                                   int R, int E, int K, int tb, uint32_t flags) {
@@ -213,8 +216,10 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
   if (valid && !isfinite(wv)) flags |= 2u;
   const int id = ok ? idv : 0;
   uint64_t match = __ballot(ok);
+  const int nbits = id_bits(E);
 #pragma unroll
   for (int bit = 0; bit < 8; ++bit) {
+    if (bit >= nbits) break;  // every id is below 2^nbits
     const bool set = (id >> bit) & 1;
     const uint64_t b = __ballot(ok && set);
     match &= set ? b : ~b;
@@ -222,23 +227,25 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
   const int lrank = __popcll(match & lanemask_lt());
   if (ok && lrank == 0) s.wcnt[wave * E + id] = __popcll(match);
   __syncthreads();
-  for (int e = tid; e < E; e += kSmallPlanRoutes) {
-    int c = 0;
-#pragma unroll
-    for (int w = 0; w < kSmallPlanWaves; ++w) {
-      const int t = s.wcnt[w * E + e];
-      s.wcnt[w * E + e] = c;
-      c += t;
-    }
-    s.cnt[e] = c;
-  }
-  __syncthreads();
-  if (wave == 0) {  // exclusive scans of counts and task counts, four experts per lane
+  if (wave == 0) {
+    // Per expert (four per lane): counts of the waves holding routes ->
+    // exclusive prefixes in place, then exclusive scans of the counts and
+    // task counts over the experts.
+    const int nw = (R + kWave - 1) / kWave;
     int c[4], nt[4], csum = 0, tsum = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = lane * 4 + j;
-      c[j] = e < E ? s.cnt[e] : 0;
+      int run = 0;
+      if (e < E) {
+        for (int w = 0; w < nw; ++w) {
+          const int t = s.wcnt[w * E + e];
+          s.wcnt[w * E + e] = run;
+          run += t;
+        }
+        s.cnt[e] = run;
+      }
+      c[j] = run;
       nt[j] = (c[j] + tb - 1) / tb;
       csum += c[j];
       tsum += nt[j];
