@@ -108,9 +108,10 @@ const char *moe_last_error(void);
 /* Workspace size and layout for a descriptor (pointers may be NULL). */
 int moe_workspace_layout(const moe_desc *d, moe_layout *out);
 
-/* Validate the descriptor and bind its pointers.  No allocation, no launch;
- * for T > 0 it zeroes the 16-byte work-counter area of the workspace with a
- * synchronous hipMemset (every launch then leaves it at zero). */
+/* Validate the descriptor and bind its pointers.  No allocation, no launch,
+ * no device work (so it may run during stream capture).  The workspace must
+ * have been zeroed once before its first forward: its work counters start at
+ * zero and every launch leaves them at zero. */
 int moe_plan_create(moe_plan **out, const moe_desc *d);
 /* Enqueue one forward on `stream` (hipStream_t; NULL = default stream).
  * No host sync and no allocation; T == 0 launches nothing. */

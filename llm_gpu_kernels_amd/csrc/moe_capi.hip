@@ -229,12 +229,6 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
     delete p;
     return hip_fail(e, "device query");
   }
-  // The streaming GEMMs' work counters start at zero; every launch leaves
-  // them at zero.
-  if (d->T > 0 && (e = hipMemset((char *)d->workspace + L.counters, 0, 4 * sizeof(int32_t))) != hipSuccess) {
-    delete p;
-    return hip_fail(e, "zeroing the work counters");
-  }
   *out = p;
   return MOE_OK;
 }
