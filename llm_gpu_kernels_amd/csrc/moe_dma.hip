@@ -79,7 +79,7 @@ constexpr int kPlanTaskMax = route_dev::kMaxExperts + route_dev::kSmallPlanRoute
 constexpr int kPlanBytes = kPlanTaskMax * 16 + (route_dev::kSmallPlanRoutes + 64) * 4 + 16;
 
 // Work distribution.  Workgroup b first takes units A b .. A b + A - 1; every
-// later unit comes from a device-wide counter, kChunk consecutive units per
+// later unit comes from a device-wide counter, kChunkOf consecutive units per
 // atomic add, so a workgroup that streams faster takes more units (static
 // blocks of equal size measured a 20 us spread of finish times at T = 17, and
 // T = 193 gate/up 145 -> 135 us with the counter).  MFMA wave 0 takes the
@@ -90,8 +90,10 @@ constexpr int kPlanBytes = kPlanTaskMax * 16 + (route_dev::kSmallPlanRoutes + 64
 constexpr int kSeqRing = 8;
 // Units per counter step: pairs of consecutive units (fewer task switches)
 // measured 2-8 us faster per launch than single units at T = 17 and 193, and
-// than larger blocks, which leave longer tails.
-constexpr int kChunk = 2;
+// than larger blocks, which leave longer tails; the 32-row units of down
+// with 32-row tasks go in fours (T = 300-480: down 3-7 us faster than pairs).
+template <int KIND, int MT>
+constexpr int kChunkOf = KIND == 1 && MT == 2 ? 4 : 2;
 
 __device__ __forceinline__ void finish_units(int32_t *w, int G) {
   if (atomicAdd(w + 1, 1) == G - 1) {
@@ -440,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
             pending = false;
           }
           if (taking) {  // unit i + A
-            if (lane == 0) taken = (i % kChunk) ? taken + 1 : kChunk * atomicAdd(wcnt, 1);
+            if (lane == 0) taken = (i % kChunkOf<KIND, MT>) ? taken + 1 : kChunkOf<KIND, MT> * atomicAdd(wcnt, 1);
             pending = true;
           }
         }

@@ -347,13 +347,13 @@ def test_fused_router_two_tokens_per_wave(tokens, experts, k, gpu_device):
     assert plan.read_status() & 4
 
 
-@pytest.mark.parametrize("tokens", [17, 193])
+@pytest.mark.parametrize("tokens", [17, 193, 384])
 def test_work_counters_return_to_zero(tokens, gpu_device):
     """Qwen shape, bf16: the LDS-streaming gate/up and down launches hand out
     units from device-wide counters that the last workgroup of each launch
     resets.  After every forward the counters read zero, and forwards over
     new tokens (T = 17: routed in the gate/up prologue; T = 193: planner
-    launch) each match the oracle -- a unit skipped or taken twice by a
+    launch; T = 384: 32-row tasks) each match the oracle -- a unit skipped or taken twice by a
     stale counter would leave the previous forward's rows in the output."""
     lay = make_layer("qwen", tokens, seed=50 + tokens, device=gpu_device)
     g = torch.Generator().manual_seed(tokens)
