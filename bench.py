@@ -86,46 +86,61 @@ FORWARDS_PER_GRAPH = 8
 
 
 def time_layer(plans, steps, warmup):
-    """Average ms per forward over exactly `steps` forwards.  A HIP graph holds
-    FORWARDS_PER_GRAPH forwards that alternate between the weight copies
-    (BASELINE's protocol: graph replays of 8 forwards / 8); a second graph holds
-    the remainder steps % 8.  p50/p95 come from per-replay samples / 8."""
+    """Time exactly `steps` forwards; returns (ms per forward, per-graph samples).
+
+    BASELINE's protocol (benchmark.py:68-98 of the reference): HIP graphs of
+    FORWARDS_PER_GRAPH forwards, device time from HIP events on the replay
+    stream.  Two graphs alternate the two weight copies in opposite orders
+    (A B A B ... and B A B A ...), and replays alternate between them (AB/BA
+    rounds), so neither copy always runs first.  A third graph holds the
+    remainder steps % 8.  Warmup replays at least max(W, 32) forwards so the
+    timed region starts at steady clocks.  Every full replay inside the timed
+    region is also an event-timed sample (/8), and 16 more replays after it
+    give p50/p95; the mean is total time / steps over the timed region."""
     stream = torch.cuda.Stream()
     for p in plans:
         for _ in range(2):
             p.run()
     torch.cuda.synchronize()
 
-    def capture(n):
+    def capture(n, first):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             for i in range(n):
-                plans[i % len(plans)].run()
+                plans[(first + i) % len(plans)].run()
         return graph
 
-    full = capture(FORWARDS_PER_GRAPH)
+    rounds = [capture(FORWARDS_PER_GRAPH, 0), capture(FORWARDS_PER_GRAPH, 1)]
     replays, rem = divmod(steps, FORWARDS_PER_GRAPH)
-    tail = capture(rem) if rem else None
-    for _ in range(max(1, -(-warmup // FORWARDS_PER_GRAPH))):
-        full.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        full.replay()
-    if tail is not None:
+    tail = capture(rem, replays % 2) if rem else None
+    for i in range(max(4, -(-warmup // FORWARDS_PER_GRAPH))):
+        rounds[i % 2].replay()
+    if tail is not None:  # a graph's first replay also uploads it
         tail.replay()
-    end.record()
+        tail.replay()
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    samples = []
-    for _ in range(20):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        full.replay()
-        b.record()
-        b.synchronize()
-        samples.append(a.elapsed_time(b) / FORWARDS_PER_GRAPH)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    marks = [ev() for _ in range(replays + 1)]
+    end = ev()
+    with torch.cuda.stream(stream):
+        marks[0].record(stream)
+        for i in range(replays):
+            rounds[i % 2].replay()
+            marks[i + 1].record(stream)
+        if tail is not None:
+            tail.replay()
+        end.record(stream)
+    end.synchronize()
+    total_ms = marks[0].elapsed_time(end)
+    samples = [marks[i].elapsed_time(marks[i + 1]) / FORWARDS_PER_GRAPH for i in range(replays)]
+    extra = [ev() for _ in range(17)]
+    with torch.cuda.stream(stream):
+        extra[0].record(stream)
+        for i in range(16):
+            rounds[i % 2].replay()
+            extra[i + 1].record(stream)
+    extra[-1].synchronize()
+    samples += [extra[i].elapsed_time(extra[i + 1]) / FORWARDS_PER_GRAPH for i in range(16)]
     return total_ms / max(steps, 1), samples
 
 
@@ -157,9 +172,9 @@ def measure(name, steps, warmup, device):
     lay, plans = build_plans(spec, device)
     alg = algorithmic(spec, lay, plans[0])
     ms, samples = time_layer(plans, steps, warmup)
-    gate_idx = plans[0].launches.index("gate_up_swiglu")
+    gate_idx = plans[0].launch_names.index("gate_up_swiglu")
     gu_ms = time_stage(plans, gate_idx)
-    stage_ms = {n: round(time_stage(plans, i, reps=20) * 1e3, 2) for i, n in enumerate(plans[0].launches)}
+    stage_ms = {n: round(time_stage(plans, i, reps=20) * 1e3, 2) for i, n in enumerate(plans[0].launch_names)}
     t = spec["T"]
     layer_gbs = alg["layer_bytes"] / (ms * 1e-3) / 1e9
     tflops = alg["flops"] / (ms * 1e-3) / 1e12
@@ -219,24 +234,52 @@ def measure_attention(tokens, device, reps=20, per_graph=10):
                 arithmetic_intensity=round(flops / nbytes, 1))
 
 
-def cpu_baseline(lay, spec, budget_s=12.0):
-    """FP32 CPU oracle (reference.py:17-45 restated) + CPU router, bounded sample."""
-    from oracle.moe_oracle import moe_reference, route_topk
-    x, gu, dn, logits = (lay["x"].cpu(), lay["gate_up"].cpu(), lay["down"].cpu(),
-                         lay["logits"].cpu())
+def _cpu_sample(fn, budget_s, max_runs):
+    """Mean seconds of fn() over a bounded sample (at least one run)."""
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 20:
+    while not times or (time.perf_counter() < t_end and len(times) < max_runs):
         t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.mean(times), len(times)
+
+
+def cpu_baseline(lay, spec, budget_s=10.0, max_runs=20):
+    """FP32 CPU oracle (reference.py:17-45 restated) + CPU router, bounded
+    sample, on this host's cores.  W4 layers run it on the dequantised
+    gate/up weights (dequantised once, outside the timed sample)."""
+    from oracle.moe_oracle import dequantize_w4, moe_reference, route_topk
+    x, dn, logits = lay["x"].cpu(), lay["down"].cpu(), lay["logits"].cpu()
+    gu = lay["gate_up"].cpu()
+    if spec["w4"]:
+        from llm_gpu_kernels_amd import quantize_gate_up
+        packed = quantize_gate_up(gu)
+        gu = dequantize_w4(packed.words, packed.scales)
+
+    def forward():
         ids, w = route_topk(logits, lay["K"])
         moe_reference(x, gu, dn, ids, w)
-        times.append(time.perf_counter() - t0)
-    mean = statistics.mean(times)
+
+    mean, n = _cpu_sample(forward, budget_s, max_runs)
     return {"value": round(spec["T"] / mean, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port", "us_per_layer": round(mean * 1e6, 1),
-            "sample": f"{len(times)} full forwards of the {spec['shape']} T={spec['T']} layer "
+            "sample": f"{n} full forwards of the {spec['shape']} T={spec['T']} layer "
                       f"(oracle.moe_oracle.route_topk + moe_reference, FP32, torch CPU, "
-                      f"os.cpu_count()={os.cpu_count()})"}
+                      f"{torch.get_num_threads()} threads, os.cpu_count()={os.cpu_count()})"}
+
+
+def cpu_attention_baseline(tokens, budget_s=3.0):
+    """FP32 SDPA-math oracle of the segmented GQA attention (the reference's
+    own test oracle, tests/e2e/test_compact_attention.py:49-78) on this host."""
+    from oracle.moe_oracle import gqa_segmented_reference
+    g = torch.Generator().manual_seed(tokens)
+    rnd = lambda shape: torch.randn(shape, generator=g).to(torch.bfloat16)
+    q = rnd((tokens, 32, 128))
+    segs = [(rnd((L, 8, 128)), rnd((L, 8, 128))) for L in (1024, 512, 256, tokens)]
+    mean, n = _cpu_sample(lambda: gqa_segmented_reference(q, segs), budget_s, 50)
+    return {"cpu_us": round(mean * 1e6, 1), "cpu_cores": torch.get_num_threads(),
+            "cpu_sample": f"{n} calls of oracle.moe_oracle.gqa_segmented_reference (FP32)"}
 
 
 def copy_calibration(mib: int):
@@ -265,6 +308,14 @@ def profiled_traffic(workload: str):
     except OSError:
         pass
     return None
+
+
+def _attach_cpu(rec, cpu):
+    """The CPU FP32 baseline of one sweep record, in the record's own terms."""
+    rec["cpu_us_per_layer"] = cpu["us_per_layer"]
+    rec["cpu_tokens_per_s"] = cpu["value"]
+    rec["cores"] = cpu["cores"]
+    rec["cpu_sample"] = cpu["sample"]
 
 
 def main():
@@ -299,6 +350,12 @@ def main():
     log(f"[bench] workload {args.workload}")
     main_res, lay, plans = measure(args.workload, args.steps, args.warmup, device)
     spec = WORKLOADS[args.workload]
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(lay, spec)
+        _attach_cpu(main_res, cpu)
+    del plans
     sweep = []
     if not args.no_sweep:
         for name in WORKLOADS:
@@ -306,19 +363,23 @@ def main():
                 sweep.append(main_res)
                 continue
             log(f"[bench] sweep {name}")
-            r, _, p = measure(name, args.steps, args.warmup, device)
-            sweep.append(r)
+            r, lay_s, p = measure(name, args.steps, args.warmup, device)
             del p
+            if not args.no_cpu:
+                _attach_cpu(r, cpu_baseline(lay_s, WORKLOADS[name], budget_s=3.0, max_runs=10))
+            sweep.append(r)
+            del lay_s
             torch.cuda.empty_cache()
     attention = []
     if not args.no_sweep:
         for t in (32, 96, 256):
             log(f"[bench] attention T={t}")
-            attention.append(measure_attention(t, device))
-    cpu = None
-    if not args.no_cpu:
-        log("[bench] cpu baseline")
-        cpu = cpu_baseline(lay, spec)
+            rec = measure_attention(t, device)
+            if not args.no_cpu:
+                c = cpu_attention_baseline(t)
+                rec.update(c)
+                rec["cpu_tokens_per_s"] = round(t / (c["cpu_us"] * 1e-6), 1)
+            attention.append(rec)
     gu = main_res["gate_up"]
     line = {
         "metric": METRIC, "value": main_res["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,

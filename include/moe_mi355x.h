@@ -41,6 +41,11 @@ extern "C" {
 #define MOE_STATUS_BAD_ID 1u      /* an expert ID outside [0, E)              */
 #define MOE_STATUS_BAD_WEIGHT 2u  /* a non-finite routing weight              */
 #define MOE_STATUS_BAD_LOGIT 4u   /* a non-finite router logit (router mode)  */
+#define MOE_STATUS_DIRTY_COUNTERS 8u /* read_status only: the work counters were
+                                        not zero after the stream drained (a launch
+                                        that did not complete, or a workspace that
+                                        was not zeroed); moe_plan_reset_counters or
+                                        any later complete forward clears them     */
 
 /* moe_desc.weight_format */
 #define MOE_WEIGHTS_BF16 0        /* gate_up bf16 [E, 2I, H]                  */
@@ -109,15 +114,22 @@ const char *moe_last_error(void);
 int moe_workspace_layout(const moe_desc *d, moe_layout *out);
 
 /* Validate the descriptor and bind its pointers.  No allocation, no launch,
- * no device work (so it may run during stream capture).  The workspace must
- * have been zeroed once before its first forward: its work counters start at
- * zero and every launch leaves them at zero. */
+ * no device work (so it may run during stream capture).  The workspace should
+ * be zeroed once before its first forward: the streaming GEMMs hand out work
+ * from four counters that must read zero when they start.  Every complete
+ * forward leaves them at zero, and the planner and combine launches zero
+ * them as well, so a dirty workspace heals after one forward; use
+ * moe_plan_reset_counters to clean one before its first forward. */
 int moe_plan_create(moe_plan **out, const moe_desc *d);
 /* Enqueue one forward on `stream` (hipStream_t; NULL = default stream).
  * No host sync and no allocation; T == 0 launches nothing. */
 int moe_plan_run(moe_plan *p, void *stream);
-/* Synchronise `stream` and read the device status bits. */
+/* Synchronise `stream` and read the device status bits (MOE_STATUS_*). */
 int moe_plan_read_status(moe_plan *p, void *stream, uint32_t *flags);
+/* Enqueue a one-workgroup kernel that zeroes the work counters (capturable:
+ * a kernel node, not a memset).  No counterpart in the reference, whose Triton
+ * GEMMs use a static grid; for C-ABI callers that reuse workspace memory. */
+int moe_plan_reset_counters(moe_plan *p, void *stream);
 /* Enqueue launch `stage` (0 <= stage < layout.launches) of one forward alone:
  * per-kernel timing, as the reference's per-stage graphs
  * (moe_benchmark.py:258-282).  Stages read what earlier stages wrote. */

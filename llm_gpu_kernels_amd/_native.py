@@ -14,6 +14,7 @@ MOE_OK, MOE_EINVAL, MOE_EDEVICE, MOE_ESPACE = 0, -1, -2, -3
 WEIGHTS_BF16, WEIGHTS_W4G128 = 0, 1
 IDS_INT32, IDS_INT64 = 0, 1
 ROUTE_FIXED, ROUTE_LOGITS = 0, 1
+STATUS_BAD_ID, STATUS_BAD_WEIGHT, STATUS_BAD_LOGIT, STATUS_DIRTY_COUNTERS = 1, 2, 4, 8
 
 
 class MoeDesc(ctypes.Structure):
@@ -56,6 +57,7 @@ SIGNATURES = {
     "moe_plan_run": (c_int32, [c_void_p, c_void_p]),
     "moe_plan_run_stage": (c_int32, [c_void_p, c_int32, c_void_p]),
     "moe_plan_read_status": (c_int32, [c_void_p, c_void_p, POINTER(c_uint32)]),
+    "moe_plan_reset_counters": (c_int32, [c_void_p, c_void_p]),
     "moe_plan_layout": (c_int32, [c_void_p, POINTER(MoeLayout)]),
     "moe_plan_destroy": (None, [c_void_p]),
     "moe_w4_quantize": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),

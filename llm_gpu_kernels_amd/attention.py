@@ -37,6 +37,18 @@ def _validate(t, name, device, heads):
         raise ValueError(f"{name} base address must be 16-byte aligned")
 
 
+def check_out_storage(out, inputs):
+    """Reject an output that shares storage with q or a K/V segment: the kernel
+    writes out while other workgroups still read the inputs
+    (attention_cuda_compact.py:175-177 rejects the same).  Empty tensors own no
+    memory and cannot alias."""
+    if out.numel() == 0:
+        return
+    storage = out.untyped_storage().data_ptr()
+    if any(t.numel() and t.untyped_storage().data_ptr() == storage for t in inputs):
+        raise ValueError("out must not share storage with any input")
+
+
 class PreparedSegmentedGQA:
     """Owns the output and split-K workspace; binds q and the segments by address."""
 
@@ -61,6 +73,7 @@ class PreparedSegmentedGQA:
             out = torch.empty_like(q)
         if tuple(out.shape) != tuple(q.shape) or out.dtype != torch.bfloat16 or not out.is_contiguous():
             raise ValueError("out must be a contiguous bf16 tensor shaped like q")
+        check_out_storage(out, [q] + [t for pair in segments for t in pair])
         self.q, self.segments, self.output = q, segments, out
         d = N.GqaDesc()
         d.T, d.Hq, d.Hkv, d.D, d.num_segments = t, hq, hkv, 128, len(segments)
@@ -71,7 +84,7 @@ class PreparedSegmentedGQA:
             d.k_stride[i] = k.stride(0) if k.shape[0] else hkv * 128
             d.v_stride[i] = v.stride(0) if v.shape[0] else hkv * 128
         d.q, d.out = q.data_ptr(), out.data_ptr()
-        d.scale = float(scale) if scale else 1.0 / math.sqrt(128.0)
+        d.scale = float(scale) if scale is not None else 1.0 / math.sqrt(128.0)
         nbytes = ctypes.c_size_t(0)
         with torch.cuda.device(q.device):
             N.check(N.lib().gqa_seg_workspace_bytes(ctypes.byref(d), ctypes.byref(nbytes)), "prepare")

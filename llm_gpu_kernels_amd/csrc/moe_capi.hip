@@ -348,6 +348,27 @@ int moe_plan_read_status(moe_plan *p, void *stream, uint32_t *flags) {
   const char *ws = (const char *)p->d.workspace;
   e = hipMemcpy(flags, ws + p->L.status, sizeof(uint32_t), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(e, "status readback");
+  // Every completed launch leaves the work counters at zero; anything else
+  // means a launch did not run to completion on this workspace.
+  int32_t cnt[4];
+  e = hipMemcpy(cnt, ws + p->L.counters, sizeof(cnt), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "counter readback");
+  if (cnt[0] | cnt[1] | cnt[2] | cnt[3]) *flags |= MOE_STATUS_DIRTY_COUNTERS;
+  return MOE_OK;
+}
+
+int moe_plan_reset_counters(moe_plan *p, void *stream) {
+  if (!p) return fail(MOE_EINVAL, "null plan");
+  if (p->d.T == 0) return MOE_OK;
+  int prev = -1;
+  hipError_t e = hipGetDevice(&prev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (prev != p->device && (e = hipSetDevice(p->device)) != hipSuccess)
+    return hip_fail(e, "hipSetDevice");
+  e = moe::launch_reset_counters((int32_t *)((char *)p->d.workspace + p->L.counters),
+                                 (hipStream_t)stream);
+  if (prev != p->device) (void)hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(e, "counter reset");
   return MOE_OK;
 }
 

@@ -211,6 +211,9 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     l_tasks = p_tasks;
     l_row_token = p_row;
   }
+  // The planning gate/up launch is the first of its forward: it zeroes the
+  // down launch's counters (which start only after this launch ends).
+  if (PLAN && blockIdx.x == 0 && tid < 2) a.counters[2 + tid] = 0;
   const int total = (PLAN ? ntasks : *as_const(a.num_tasks)) * ncb;
   const int G = gridDim.x;
   constexpr int A = kAheadOf<NS, SPU>;
@@ -436,7 +439,8 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         if (i > 0) epilogue(prev, (i - 1) % C::PAR, (i - 1) & 1);
         if (wave == 0) {
           if (pending) {  // unit i - 1 + A, taken at the start of unit i - 1
-            const int u = __builtin_amdgcn_readfirstlane(taken) + S * G;
+            int u = __builtin_amdgcn_readfirstlane(taken) + S * G;
+            if (u < 0) u = total;  // a corrupted counter ends the workgroup's units
             if (lane == 0) seq[(i - 1 + A) % kSeqRing] = u;
             taking = u < total;
             pending = false;

@@ -22,7 +22,16 @@ namespace {
 // out[t] = bf16(sum_s fp32(routed[t*K+s]) * w[t,s]), slot order, no FMA.
 // Slots are taken eight at a time with every load of a chunk issued before
 // the first add, so a token costs one memory round trip per eight slots.
+// The combine is the last launch of every forward: it also zeroes the work
+// counters of the streaming GEMMs (their own last workgroups already do), so
+// a workspace whose counters were left nonzero -- an aborted forward, a reused
+// arena -- is clean again from the next forward on.
+__device__ __forceinline__ void clear_counters(const ExpertArgs &a) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 4) a.counters[threadIdx.x] = 0;
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(ExpertArgs a) {
+  clear_counters(a);
   const int t = blockIdx.x;
   const int h = (blockIdx.y * 256 + threadIdx.x) * 8;
   if (h >= a.H) return;
@@ -102,6 +111,7 @@ __global__ __launch_bounds__(256) void down_generic_kernel(ExpertArgs a, int tok
 }
 
 __global__ __launch_bounds__(256) void combine_generic_kernel(ExpertArgs a) {
+  clear_counters(a);
   const int t = blockIdx.x;
   const int h = blockIdx.y * 256 + threadIdx.x;
   if (h >= a.H) return;
@@ -185,6 +195,17 @@ hipError_t launch_combine(const ExpertArgs &a, hipStream_t s) {
     const dim3 grid(a.T, (a.H + 255) / 256);
     hipLaunchKernelGGL(combine_generic_kernel, grid, dim3(256), 0, s, a);
   }
+  return hipGetLastError();
+}
+
+namespace {
+__global__ void reset_counters_kernel(int32_t *c) {
+  if (threadIdx.x < 4) c[threadIdx.x] = 0;
+}
+}  // namespace
+
+hipError_t launch_reset_counters(int32_t *counters, hipStream_t s) {
+  hipLaunchKernelGGL(reset_counters_kernel, dim3(1), dim3(64), 0, s, counters);
   return hipGetLastError();
 }
 

@@ -75,6 +75,9 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   if (fmode == 2) load_token_logits<true>(a.logits, ft, ft < a.T, E, raw);
   else if (fmode == 1) load_token_logits<false>(a.logits, ft, ft < a.T, E, raw);
   if (tid == 0) sh.status = 0;
+  // The planner runs before both streaming GEMMs: their work counters start
+  // at zero even on a workspace an earlier, aborted forward left dirty.
+  if (tid < 4) a.counters[tid] = 0;
   for (int e = tid; e < E; e += kPlanThreads) sh.run[e] = 0;
   for (int i = tid; i < kPlanWaves * kMaxExperts; i += kPlanThreads) (&sh.wcnt[0][0][0])[i] = 0;
   uint32_t flags = 0;

@@ -29,7 +29,7 @@ from . import _native as N
 from .weight_quant import PackedGateUp, RepackedGateUp, TiledGateUp, tile_gate_up
 
 __all__ = [
-    "GemmConfig", "FrozenMoEPolicy", "PreparedMoE", "PreparedRoutedMoE", "prepare_moe",
+    "GemmConfig", "FrozenMoEPolicy", "MoEWorkspace", "PreparedLaunch", "PreparedMoE", "PreparedRoutedMoE", "prepare_moe",
     "prepare_ranked_moe_launcher", "prepare_configured_moe", "prepare_cuda_moe",
     "prepare_w4_moe", "prepare_w4_layout_moe", "prepare_routed_moe",
 ]
@@ -67,6 +67,49 @@ class FrozenMoEPolicy:
         if mu < 2 * self.small_mu:
             return GemmConfig(block_m=32), "medium"
         return GemmConfig(block_m=64), "large"
+
+
+@dataclass(frozen=True)
+class PreparedLaunch:
+    """One kernel launch of a prepared forward (role of ``_PreparedLaunch``,
+    moe_prepared.py:17-30): ``run()`` enqueues that launch alone on the
+    current stream; it reads what the launches before it wrote."""
+    name: str
+    stage: int
+    plan: "PreparedMoE" = field(repr=False, compare=False)
+
+    def run(self):
+        self.plan.run_stage(self.stage)
+
+
+@dataclass(frozen=True)
+class MoEWorkspace:
+    """The prepared workspace (role of the reference's ``base``: ``PreparedMoE``
+    / ``W4Workspace``, moe.py:124-156, moe_w4_cuda.py:53-82): views of the
+    bound inputs, the owned output and the device arrays of the last forward.
+    ``down_output`` holds the down projections in route order (the reference's
+    name for them); there is no ``grouped_input``, because the GEMMs gather
+    the token rows of ``x`` directly."""
+    x: torch.Tensor
+    gate_up: object
+    down: torch.Tensor
+    ids: torch.Tensor
+    routing_weights: torch.Tensor
+    output: torch.Tensor
+    counts: torch.Tensor
+    offsets: torch.Tensor
+    ranks: torch.Tensor
+    mapping: torch.Tensor
+    row_route: torch.Tensor
+    tasks: torch.Tensor
+    num_tasks: torch.Tensor
+    activated: torch.Tensor
+    down_output: torch.Tensor
+    status: torch.Tensor
+    work_counters: torch.Tensor
+    config: GemmConfig
+    workspace_bytes: int
+    check_inputs: object = field(repr=False, compare=False)
 
 
 def _device_check(tensors, device):
@@ -171,8 +214,17 @@ class PreparedMoE:
         else:
             names = (["router"] if (logits is not None and lay.launches == 5) else []) + \
                 ["route_plan", "gate_up_swiglu", "down", "combine"]
-        self.launches = tuple(names) if t else ()
+        self.launch_names = tuple(names) if t else ()
+        self.launches = tuple(PreparedLaunch(n, i, self) for i, n in enumerate(self.launch_names))
         self.fast_path = bool(lay.fast_path)
+        self.base = MoEWorkspace(
+            x=x, gate_up=gate_up if gate_up is not None else tiled, down=down, ids=ids,
+            routing_weights=routing_weights, output=self.output, counts=self.counts,
+            offsets=self.offsets, ranks=self.ranks, mapping=self.mapping,
+            row_route=self.row_route, tasks=self.tasks, num_tasks=self.num_tasks,
+            activated=self.activated, down_output=self.routed_output, status=self.status,
+            work_counters=self.work_counters, config=self.config,
+            workspace_bytes=int(lay.total), check_inputs=self.check_inputs)
 
     @property
     def workspace_bytes(self) -> int:
@@ -199,9 +251,18 @@ class PreparedMoE:
                                              ctypes.byref(flags)), "status")
         return int(flags.value)
 
+    def reset_counters(self):
+        """Enqueue a kernel that zeroes the streaming GEMMs' work counters."""
+        stream = torch.cuda.current_stream(self.x.device).cuda_stream
+        N.check(N.lib().moe_plan_reset_counters(self._plan, ctypes.c_void_p(stream)),
+                "reset_counters")
+
     def check_inputs(self):
         """Synchronising debug check of the last forward (moe.py:157-160)."""
         flags = self.read_status()
+        if flags & N.STATUS_DIRTY_COUNTERS:
+            raise RuntimeError(f"MoE workspace work counters are not zero (GPU status={flags}): "
+                               "a launch did not complete; call reset_counters()")
         if flags:
             raise ValueError(f"invalid runtime MoE inputs: GPU status={flags} "
                              "(1=IDs, 2=nonfinite weights, 4=nonfinite logits)")
@@ -241,8 +302,16 @@ def prepare_configured_moe(x, gate_up, down, ids, routing_weights, config):
     return prepare_moe(x, gate_up, down, ids, routing_weights, config=config)
 
 
-def prepare_cuda_moe(x, gate_up, down, ids, routing_weights, variant="mfma", down_config=None):
-    """Native BF16 gate/up entry (moe_cuda.py:54); one MFMA variant on gfx950."""
+# The reference's native gate/up variants (moe_cuda.py:17).  They differ only
+# in SM86 copy pipelining; on gfx950 every name selects the same MFMA kernels.
+CUDA_VARIANTS = ("sync", "async", "async_skip")
+
+
+def prepare_cuda_moe(x, gate_up, down, ids, routing_weights, *, variant="sync", down_config=None):
+    """Native BF16 gate/up entry (moe_cuda.py:54-73): the reference's variant
+    names are accepted and anything else is rejected as there."""
+    if variant not in CUDA_VARIANTS:
+        raise ValueError("unsupported CUDA variant")
     return prepare_moe(x, gate_up, down, ids, routing_weights, config=down_config)
 
 

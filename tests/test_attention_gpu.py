@@ -101,3 +101,20 @@ def test_rejects_bad_inputs(gpu_device):
         prepare_segmented_gqa(q, segs[:-1] + [(segs[-1][0][:4], segs[-1][1][:4])])
     with pytest.raises(TypeError):
         prepare_segmented_gqa(q, [(k.float(), v) for k, v in segs])
+
+
+def test_out_aliasing_rejected(gpu_device):
+    """An output sharing storage with q or a K/V segment is rejected
+    (attention_cuda_compact.py:175-177)."""
+    from llm_gpu_kernels_amd import prepare_cuda_gqa_compact
+    q = torch.randn(32, 32, 128, device=gpu_device).to(torch.bfloat16)
+    kv = torch.randn(2, 64, 8, 128, device=gpu_device).to(torch.bfloat16)
+    cur = torch.randn(2, 32, 8, 128, device=gpu_device).to(torch.bfloat16)
+    segs = [(kv[0], kv[1]), (cur[0], cur[1])]
+    with pytest.raises(ValueError, match="share storage"):
+        prepare_cuda_gqa_compact(q, segs, out=q)
+    big = torch.empty(2, 32, 32, 128, device=gpu_device, dtype=torch.bfloat16)
+    segs_alias = [(kv[0], kv[1]), (big[1, :, :8], cur[1])]
+    with pytest.raises(ValueError):
+        prepare_cuda_gqa_compact(q, segs_alias, out=big[0])
+    prepare_cuda_gqa_compact(q, segs)

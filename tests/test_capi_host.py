@@ -192,3 +192,35 @@ def test_tile_emulated_decode_matches_oracle_dequant():
                     base = grp * 128 + 32 * j + 8 * gg
                     out[0, rb * 16 + r, base:base + 8] = torch.tensor(vals).to(torch.bfloat16)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_cuda_variant_names_validated():
+    """prepare_cuda_moe accepts the reference's variant names only
+    (moe_cuda.py:17,57-58); the check precedes any device work."""
+    from llm_gpu_kernels_amd import moe as M
+    assert M.CUDA_VARIANTS == ("sync", "async", "async_skip")
+    with pytest.raises(ValueError, match="unsupported CUDA variant"):
+        M.prepare_cuda_moe(None, None, None, None, None, variant="mfma")
+
+
+def test_attention_out_storage_check():
+    """Output aliasing q or any K/V segment storage is rejected (views of one
+    storage included); empty tensors never alias."""
+    from llm_gpu_kernels_amd.attention import check_out_storage
+    q = torch.zeros(4, 32, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(2, 4, 8, 128, dtype=torch.bfloat16)
+    out = torch.zeros_like(q)
+    check_out_storage(out, [q, kv[0], kv[1]])
+    with pytest.raises(ValueError, match="share storage"):
+        check_out_storage(q, [q, kv[0], kv[1]])
+    with pytest.raises(ValueError, match="share storage"):
+        check_out_storage(kv[1], [q, kv[0]])
+    check_out_storage(torch.empty(0, 32, 128), [torch.empty(0, 8, 128)])
+
+
+def test_status_bit_values():
+    """Status bits of the header, as the Python layer reads them."""
+    text = (INCLUDE / "moe_mi355x.h").read_text()
+    for name, value in (("BAD_ID", 1), ("BAD_WEIGHT", 2), ("BAD_LOGIT", 4), ("DIRTY_COUNTERS", 8)):
+        assert re.search(rf"#define MOE_STATUS_{name} {value}u", text), name
+        assert getattr(N, f"STATUS_{name}") == value

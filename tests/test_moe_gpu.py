@@ -332,7 +332,7 @@ def test_fused_router_two_tokens_per_wave(tokens, experts, k, gpu_device):
     g = torch.Generator().manual_seed(7 * tokens + k)
     logits = torch.randint(-6, 6, (tokens, experts), generator=g).float() * 0.75
     plan = prepare_routed_moe(*_to(gpu_device, x, logits, gu, dn), k)
-    assert plan.launches[0] != "router"
+    assert plan.launch_names[0] != "router"
     out = plan.forward()
     torch.cuda.synchronize()
     ids, w = O.route_topk(logits, k)
@@ -382,7 +382,7 @@ def test_gate_up_with_planning_prologue(tokens, gpu_device):
     g = torch.Generator().manual_seed(tokens)
     logits = (torch.randint(-6, 6, (tokens, lay["E"]), generator=g).float() * 0.75).to(gpu_device)
     plan = prepare_routed_moe(lay["x"], logits, lay["gate_up"], lay["down"], 8)
-    assert plan.launches == ("gate_up_swiglu", "down", "combine")
+    assert plan.launch_names == ("gate_up_swiglu", "down", "combine")
     out = plan.forward().clone()
     torch.cuda.synchronize()
     ids, w = O.route_topk(logits.cpu(), 8)
@@ -399,3 +399,64 @@ def test_gate_up_with_planning_prologue(tokens, gpu_device):
     logits[tokens - 1, 5] = float("nan")
     plan.forward()
     assert plan.read_status() & 4
+
+
+QWEN_PERF = [c for c in GOLDEN["cases"] if c["family"] == "performance_cases" and c["E"] == 128]
+
+
+@pytest.mark.parametrize("case", QWEN_PERF, ids=lambda c: c["name"])
+def test_reference_qwen_shape_cases(case, gpu_device):
+    """The reference's recorded Qwen3-30B-A3B-shape performance cases
+    (moe_benchmark.py:380-400; routing digests in the golden records) through
+    the MFMA kernels: dispatch bit-exact with the canonical one and the recorded
+    counts/offsets, the output within the reference's limits of the FP32
+    oracle and within 2e-3/8e-3 of the rounding-staged oracle; then the same
+    routes through the W4 path against the FP32 oracle on the dequantised
+    weights."""
+    x, gu, dn, ids, rw = O.make_inputs(tokens=case["T"], experts=128, topk=8, hidden=2048,
+                                       intermediate=768, id_dtype=torch.int32,
+                                       pattern=case["route_pattern"], seed=case["seed"])
+    assert O.tensor_hash(ids) == case["routing_sha256"]
+    dev = _to(gpu_device, x, gu, dn, ids, rw)
+    plan = prepare_moe(*dev)
+    assert plan.layout.fast_path == 1
+    out = plan.run().clone()
+    torch.cuda.synchronize()
+    plan.check_inputs()
+    _check_dispatch(plan, ids, 128)
+    assert plan.counts.cpu().tolist() == case["expected_counts"]
+    assert plan.offsets.cpu().tolist() == case["expected_offsets"]
+    m32 = O.error(out, O.moe_reference(x, gu, dn, ids, rw), REF_LIMITS)
+    assert m32["passed"], m32
+    ms = O.error(out, O.staged_bf16_oracle(x, gu, dn, ids, rw), STAGED_LIMITS)
+    assert ms["passed"], ms
+    packed = quantize_gate_up(gu)
+    w4 = prepare_w4_moe(dev[0], packed, dev[2], dev[3], dev[4])
+    out4 = w4.run().clone()
+    torch.cuda.synchronize()
+    w4.check_inputs()
+    m4 = O.error(out4, O.moe_reference(x, O.dequantize_w4(packed.words, packed.scales), dn, ids, rw))
+    assert m4["passed"], m4
+
+
+def test_launch_objects_and_workspace_view(gpu_device):
+    """``launches`` are launch objects whose ``run()`` enqueues one stage (the
+    reference's _PreparedLaunch, moe_prepared.py:17-30): running them in order
+    equals ``run()``.  ``base`` exposes the workspace arrays by the reference's
+    names (moe.py:124-156)."""
+    lay = make_layer("qwen", 193, seed=21, device=gpu_device)
+    plan = prepare_routed_moe(lay["x"], lay["logits"], lay["gate_up"], lay["down"], 8)
+    ref = plan.run().clone()
+    plan.output.zero_()
+    for launch in plan.launches:
+        launch.run()
+    torch.cuda.synchronize()
+    assert [l.name for l in plan.launches] == list(plan.launch_names)
+    assert torch.equal(plan.output.view(torch.int16), ref.view(torch.int16))
+    base = plan.base
+    assert base.output.data_ptr() == plan.output.data_ptr()
+    assert torch.equal(base.counts.cpu(), torch.bincount(plan.ids.cpu().flatten().long(),
+                                                         minlength=128).int())
+    assert base.mapping.numel() == 193 * 8 and base.down_output.shape == (193 * 8, 2048)
+    assert base.workspace_bytes == plan.workspace_bytes
+    base.check_inputs()
