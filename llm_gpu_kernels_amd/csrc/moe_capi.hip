@@ -126,7 +126,11 @@ moe_layout compute_layout(const moe_desc *d) {
     o = align_up(o + bytes, 256);
     return at;
   };
+  // status and counters first: at fixed offsets for every shape, so memory
+  // reused across shapes (the static workspace) keeps them where the last
+  // forward left them zero.
   L.status = take(2 * sizeof(uint32_t));
+  L.counters = take(4 * 4);
   L.counts = take((size_t)d->E * 4);
   L.offsets = take((size_t)d->E * 4);
   L.ranks = take(R * 4);
@@ -135,7 +139,6 @@ moe_layout compute_layout(const moe_desc *d) {
   L.row_token = take(R * 4 + 64 * 4);
   L.tasks = take(cap * 16);
   L.num_tasks = take(4);
-  L.counters = take(4 * 4);
   L.act = take(R * (size_t)d->I * 2);
   L.routed = take(R * (size_t)d->H * 2);
   L.total = o;
@@ -168,23 +171,11 @@ struct moe_plan {
   int path;
 };
 
-extern "C" {
+namespace {
 
-int moe_abi_version(void) { return MOE_ABI_VERSION; }
-
-const char *moe_last_error(void) { return g_err; }
-
-int moe_workspace_layout(const moe_desc *d, moe_layout *out) {
-  int rc = validate(d);
-  if (rc) return rc;
-  if (!out) return fail(MOE_EINVAL, "null layout");
-  *out = compute_layout(d);
-  return MOE_OK;
-}
-
-int moe_plan_create(moe_plan **out, const moe_desc *d) {
-  if (!out) return fail(MOE_EINVAL, "null plan pointer");
-  *out = nullptr;
+// Validate `d` and fill `p` (no allocation, no device work).  The workspace
+// pointer and size are checked against the layout the descriptor needs.
+int bind_plan(moe_plan *p, const moe_desc *d) {
   int rc = validate(d);
   if (rc) return rc;
   const moe_layout L = compute_layout(d);
@@ -213,8 +204,6 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
   if (!fast) path = moe::kGeneric;
   if (!fast && d->weight_format == MOE_WEIGHTS_W4G128)
     return fail(MOE_EINVAL, "W4G128 buffers must be 16-byte aligned");
-  moe_plan *p = new (std::nothrow) moe_plan;
-  if (!p) return fail(MOE_EINVAL, "out of host memory");
   p->d = *d;
   p->L = L;
   p->L.fast_path = path;
@@ -225,10 +214,34 @@ int moe_plan_create(moe_plan **out, const moe_desc *d) {
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess)
     e = hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
-  if (e != hipSuccess) {
-    delete p;
-    return hip_fail(e, "device query");
-  }
+  if (e != hipSuccess) return hip_fail(e, "device query");
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_abi_version(void) { return MOE_ABI_VERSION; }
+
+const char *moe_last_error(void) { return g_err; }
+
+int moe_workspace_layout(const moe_desc *d, moe_layout *out) {
+  int rc = validate(d);
+  if (rc) return rc;
+  if (!out) return fail(MOE_EINVAL, "null layout");
+  *out = compute_layout(d);
+  return MOE_OK;
+}
+
+int moe_plan_create(moe_plan **out, const moe_desc *d) {
+  if (!out) return fail(MOE_EINVAL, "null plan pointer");
+  *out = nullptr;
+  moe_plan tmp;
+  int rc = bind_plan(&tmp, d);
+  if (rc) return rc;
+  moe_plan *p = new (std::nothrow) moe_plan(tmp);
+  if (!p) return fail(MOE_EINVAL, "out of host memory");
   *out = p;
   return MOE_OK;
 }
@@ -365,7 +378,7 @@ int moe_plan_reset_counters(moe_plan *p, void *stream) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (prev != p->device && (e = hipSetDevice(p->device)) != hipSuccess)
     return hip_fail(e, "hipSetDevice");
-  e = moe::launch_reset_counters((int32_t *)((char *)p->d.workspace + p->L.counters),
+  e = moe::launch_reset_counters((int32_t *)((char *)p->d.workspace + p->L.counters), nullptr,
                                  (hipStream_t)stream);
   if (prev != p->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(e, "counter reset");

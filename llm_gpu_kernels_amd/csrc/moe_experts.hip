@@ -199,13 +199,14 @@ hipError_t launch_combine(const ExpertArgs &a, hipStream_t s) {
 }
 
 namespace {
-__global__ void reset_counters_kernel(int32_t *c) {
+__global__ void reset_counters_kernel(int32_t *c, uint32_t *status) {
   if (threadIdx.x < 4) c[threadIdx.x] = 0;
+  if (status && threadIdx.x >= 4 && threadIdx.x < 6) status[threadIdx.x - 4] = 0;
 }
 }  // namespace
 
-hipError_t launch_reset_counters(int32_t *counters, hipStream_t s) {
-  hipLaunchKernelGGL(reset_counters_kernel, dim3(1), dim3(64), 0, s, counters);
+hipError_t launch_reset_counters(int32_t *counters, uint32_t *status, hipStream_t s) {
+  hipLaunchKernelGGL(reset_counters_kernel, dim3(1), dim3(64), 0, s, counters, status);
   return hipGetLastError();
 }
 

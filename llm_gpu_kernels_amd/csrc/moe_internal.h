@@ -77,8 +77,9 @@ bool tile_shape_ok(int H, int I, bool w4);
 // Expert-stage kernel families (moe_layout.fast_path).
 enum Path { kGeneric = 0, kStream = 1, kTile = 2 };
 hipError_t launch_combine(const ExpertArgs &a, hipStream_t s);
-// Zero the four work counters with a kernel (capturable; no memset node).
-hipError_t launch_reset_counters(int32_t *counters, hipStream_t s);
+// Zero the four work counters (and, when `status` is not null, the two
+// status words) with a kernel: capturable, no memset node.
+hipError_t launch_reset_counters(int32_t *counters, uint32_t *status, hipStream_t s);
 hipError_t launch_w4_dequantize(const uint32_t *words_t, const uint16_t *scales_t, int E, int N,
                                 int K, uint16_t *out, hipStream_t s);
 
