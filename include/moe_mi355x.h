@@ -135,6 +135,21 @@ int moe_plan_reset_counters(moe_plan *p, void *stream);
  * (moe_benchmark.py:258-282).  Stages read what earlier stages wrote. */
 int moe_plan_run_stage(moe_plan *p, int32_t stage, void *stream);
 int moe_plan_layout(const moe_plan *p, moe_layout *out);
+
+/* One forward that allocates nothing.  No counterpart in the reference: for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  `d` is as for
+ * moe_plan_create except that d->workspace and d->workspace_bytes are
+ * ignored: the workspace is a static device array of
+ * MOE_STATIC_WORKSPACE_BYTES per GPU, held until the process ends.  Shapes
+ * whose moe_workspace_layout().total exceeds it fail with MOE_ESPACE (Qwen3
+ * E128/H2048/I768/K8: T <= 371).  Enqueues a counter-reset kernel and the
+ * forward's launches on `stream`; no plan object, no host sync.  All calls on
+ * one GPU share the array: calls that overlap on one GPU (different streams,
+ * or host threads, without ordering) race, and the workspace arrays read
+ * back after a call hold that call's values only until the next one. */
+#define MOE_STATIC_WORKSPACE_BYTES (16u << 20)
+int moe_forward_static(const moe_desc *d, void *stream);
 void moe_plan_destroy(moe_plan *p);
 
 /* ---- W4G128 weights (host functions, no GPU needed) ------------------------

@@ -58,6 +58,7 @@ SIGNATURES = {
     "moe_plan_run_stage": (c_int32, [c_void_p, c_int32, c_void_p]),
     "moe_plan_read_status": (c_int32, [c_void_p, c_void_p, POINTER(c_uint32)]),
     "moe_plan_reset_counters": (c_int32, [c_void_p, c_void_p]),
+    "moe_forward_static": (c_int32, [POINTER(MoeDesc), c_void_p]),
     "moe_plan_layout": (c_int32, [c_void_p, POINTER(MoeLayout)]),
     "moe_plan_destroy": (None, [c_void_p]),
     "moe_w4_quantize": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),

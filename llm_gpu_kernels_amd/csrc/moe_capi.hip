@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 
 #include "../../include/moe_mi355x.h"
@@ -218,6 +219,32 @@ int bind_plan(moe_plan *p, const moe_desc *d) {
   return MOE_OK;
 }
 
+// ---- workspace for callers that cannot allocate ---------------------------
+// One array per GPU the library runs on, held until the process ends.  Host
+// code never uses the array's name as an address: the device address comes
+// from hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kStaticWorkspaceBytes = MOE_STATIC_WORKSPACE_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticWorkspaceBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on `device` (current), looked up on first use.
+int static_workspace(int device, void **ptr) {
+  if (device < 0 || device >= kMaxDevices) return fail(MOE_EINVAL, "device %d out of range", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(MOE_EDEVICE, "null static workspace address");
+    g_scratch_ptr[device] = p;
+  }
+  *ptr = g_scratch_ptr[device];
+  return MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -368,6 +395,35 @@ int moe_plan_read_status(moe_plan *p, void *stream, uint32_t *flags) {
   if (e != hipSuccess) return hip_fail(e, "counter readback");
   if (cnt[0] | cnt[1] | cnt[2] | cnt[3]) *flags |= MOE_STATUS_DIRTY_COUNTERS;
   return MOE_OK;
+}
+
+int moe_forward_static(const moe_desc *d, void *stream) {
+  if (!d) return fail(MOE_EINVAL, "null descriptor");
+  int rc = validate(d);
+  if (rc) return rc;
+  if (d->T == 0) return MOE_OK;
+  const moe_layout L = compute_layout(d);
+  if (L.total > kStaticWorkspaceBytes)
+    return fail(MOE_ESPACE,
+                "moe_forward_static: this shape needs %zu workspace bytes; the static "
+                "workspace holds %zu (use moe_plan_create with a caller workspace)",
+                L.total, kStaticWorkspaceBytes);
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  void *ws = nullptr;
+  if ((rc = static_workspace(device, &ws))) return rc;
+  moe_desc sd = *d;
+  sd.workspace = ws;
+  sd.workspace_bytes = kStaticWorkspaceBytes;
+  moe_plan p;
+  if ((rc = bind_plan(&p, &sd))) return rc;
+  // The array keeps the previous call's contents: the work counters and the
+  // status words must start at zero.
+  e = moe::launch_reset_counters((int32_t *)((char *)ws + L.counters),
+                                 (uint32_t *)((char *)ws + L.status), (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "static workspace reset");
+  return run_stages(&p, 0, p.L.launches, stream);
 }
 
 int moe_plan_reset_counters(moe_plan *p, void *stream) {
