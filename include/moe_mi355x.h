@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 1
+#define MOE_ABI_VERSION 2
 
 /* Return codes. */
 #define MOE_OK 0
@@ -41,6 +41,8 @@ extern "C" {
 #define MOE_STATUS_BAD_ID 1u      /* an expert ID outside [0, E)              */
 #define MOE_STATUS_BAD_WEIGHT 2u  /* a non-finite routing weight              */
 #define MOE_STATUS_BAD_LOGIT 4u   /* a non-finite router logit (router mode)  */
+#define MOE_STATUS_STALLED 16u    /* a bounded cross-workgroup wait of the planner
+                                     ran out (never expected; results invalid)   */
 #define MOE_STATUS_DIRTY_COUNTERS 8u /* read_status only: the work counters were
                                         not zero after the stream drained (a launch
                                         that did not complete, or a workspace that
@@ -82,7 +84,7 @@ typedef struct moe_desc {
 
 /* Byte offsets of the inspectable workspace arrays (int32 unless noted). */
 typedef struct moe_layout {
-  size_t status;      /* [1]  uint32 status bits                                 */
+  size_t status;      /* [4]  uint32: status bits, router bits, planner epoch, 0  */
   size_t counts;      /* [E]  routes per expert                                  */
   size_t offsets;     /* [E]  exclusive scan of counts                           */
   size_t ranks;       /* [R]  expert-local rank of route q = t*K + s (-1: bad id) */
@@ -92,15 +94,19 @@ typedef struct moe_layout {
   size_t tasks;       /* [task_capacity][4] {expert, first row, rows, 0}         */
   size_t num_tasks;   /* [1]                                                     */
   size_t counters;    /* [4]  work counters of the streaming GEMMs (0 between launches) */
+  size_t partials;    /* [W][E+1] uint32 per-workgroup counts of the multi-workgroup
+                         planner, tagged with the planner epoch                    */
   size_t act;         /* [R, I] bf16 SwiGLU activations in grouped-row order     */
   size_t routed;      /* [R, H] bf16 down projections in route order             */
   size_t total;       /* workspace bytes                                          */
   int32_t task_capacity;
   int32_t token_block;
-  int32_t launches;   /* kernel launches per forward: 5 router, plan, gate/up,   *
-                       * down, combine; 4 with the router fused into the planner *
-                       * or fixed routes; 3 when the bf16 gate/up launch routes  *
-                       * and plans itself (T <= 32); 0 when T == 0               */
+  int32_t launches;   /* kernel launches per forward: 4 route+plan, gate/up,     *
+                       * down, combine (one planner launch routes too); 3 when   *
+                       * the bf16 gate/up launch routes and plans itself         *
+                       * (T <= 32); 5 (separate router launch) only for shapes   *
+                       * with more tokens than the planner's workgroups hold     *
+                       * (T > 16 x CU count); 0 when T == 0                      */
   int32_t fast_path;  /* 0 generic kernels (unaligned shapes), 1 MFMA weight      
                          streaming, 2 MFMA LDS-tiled (many rows per expert)     */
 } moe_layout;
@@ -126,8 +132,8 @@ int moe_plan_create(moe_plan **out, const moe_desc *d);
 int moe_plan_run(moe_plan *p, void *stream);
 /* Synchronise `stream` and read the device status bits (MOE_STATUS_*). */
 int moe_plan_read_status(moe_plan *p, void *stream, uint32_t *flags);
-/* Enqueue a one-workgroup kernel that zeroes the work counters (capturable:
- * a kernel node, not a memset).  No counterpart in the reference, whose Triton
+/* Enqueue a kernel that zeroes the work counters and the planner's published
+ * per-workgroup counts (capturable: a kernel node, not a memset).  No counterpart in the reference, whose Triton
  * GEMMs use a static grid; for C-ABI callers that reuse workspace memory. */
 int moe_plan_reset_counters(moe_plan *p, void *stream);
 /* Enqueue launch `stage` (0 <= stage < layout.launches) of one forward alone:
@@ -143,7 +149,7 @@ int moe_plan_layout(const moe_plan *p, moe_layout *out);
  * ignored: the workspace is a static device array of
  * MOE_STATIC_WORKSPACE_BYTES per GPU, held until the process ends.  Shapes
  * whose moe_workspace_layout().total exceeds it fail with MOE_ESPACE (Qwen3
- * E128/H2048/I768/K8: T <= 371).  Enqueues a counter-reset kernel and the
+ * E128/H2048/I768/K8: T <= 370).  Enqueues a counter-reset kernel and the
  * forward's launches on `stream`; no plan object, no host sync.  All calls on
  * one GPU share the array: calls that overlap on one GPU (different streams,
  * or host threads, without ordering) race, and the workspace arrays read

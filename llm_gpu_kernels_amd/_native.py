@@ -14,7 +14,7 @@ MOE_OK, MOE_EINVAL, MOE_EDEVICE, MOE_ESPACE = 0, -1, -2, -3
 WEIGHTS_BF16, WEIGHTS_W4G128 = 0, 1
 IDS_INT32, IDS_INT64 = 0, 1
 ROUTE_FIXED, ROUTE_LOGITS = 0, 1
-STATUS_BAD_ID, STATUS_BAD_WEIGHT, STATUS_BAD_LOGIT, STATUS_DIRTY_COUNTERS = 1, 2, 4, 8
+STATUS_BAD_ID, STATUS_BAD_WEIGHT, STATUS_BAD_LOGIT, STATUS_DIRTY_COUNTERS, STATUS_STALLED = 1, 2, 4, 8, 16
 
 
 class MoeDesc(ctypes.Structure):
@@ -30,10 +30,12 @@ class MoeDesc(ctypes.Structure):
 class MoeLayout(ctypes.Structure):
     _fields_ = [(name, c_size_t) for name in
                 ("status", "counts", "offsets", "ranks", "map", "row_route", "row_token", "tasks",
-                 "num_tasks", "counters", "act", "routed", "total")] + \
+                 "num_tasks", "counters", "partials", "act", "routed", "total")] + \
                [("task_capacity", c_int32), ("token_block", c_int32), ("launches", c_int32),
                 ("fast_path", c_int32)]
 
+
+STATIC_WORKSPACE_BYTES = 16 << 20  # MOE_STATIC_WORKSPACE_BYTES
 
 GQA_MAX_SEGMENTS = 4
 
@@ -88,7 +90,7 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.moe_abi_version() != 1:
+        if handle.moe_abi_version() != 2:
             raise RuntimeError("libmoe_mi355x ABI version mismatch")
         _LIB = handle
     return _LIB

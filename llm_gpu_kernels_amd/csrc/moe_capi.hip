@@ -109,9 +109,19 @@ bool planned_gate_up(const moe_desc *d, int path, int tb) {
          moe::dma_plan_ok(d->H, d->I, d->T, d->K, d->E, fuse_router_mode(d));
 }
 
-int launch_count(const moe_desc *d, int path, int tb) {
+// Shapes the single-workgroup planner does not route itself (T > 32 with
+// logits, every fixed-route shape) route and plan in one launch of several
+// workgroups, all resident at once (at most one per CU).
+constexpr int kAssumedCUs = 256;  // MI355X; plans use the device's own count
+bool multi_planner(const moe_desc *d, int path, int tb, int num_cus) {
+  if (planned_gate_up(d, path, tb) || fuse_router_mode(d) != 0) return false;
+  return moe::multi_plan_ok(d->T, d->K, d->route_mode == MOE_ROUTE_LOGITS, num_cus);
+}
+
+int launch_count(const moe_desc *d, int path, int tb, int num_cus) {
   if (d->T == 0) return 0;
   if (planned_gate_up(d, path, tb)) return 3;  // gate/up (planning), down, combine
+  if (multi_planner(d, path, tb, num_cus)) return 4;  // route+plan, gate/up, down, combine
   return 4 + (d->route_mode == MOE_ROUTE_LOGITS && fuse_router_mode(d) == 0 ? 1 : 0);
 }
 
@@ -130,7 +140,7 @@ moe_layout compute_layout(const moe_desc *d) {
   // status and counters first: at fixed offsets for every shape, so memory
   // reused across shapes (the static workspace) keeps them where the last
   // forward left them zero.
-  L.status = take(2 * sizeof(uint32_t));
+  L.status = take(4 * sizeof(uint32_t));
   L.counters = take(4 * 4);
   L.counts = take((size_t)d->E * 4);
   L.offsets = take((size_t)d->E * 4);
@@ -140,13 +150,18 @@ moe_layout compute_layout(const moe_desc *d) {
   L.row_token = take(R * 4 + 64 * 4);
   L.tasks = take(cap * 16);
   L.num_tasks = take(4);
+  {
+    const int tpw = moe::multi_plan_tokens(d->K, d->route_mode == MOE_ROUTE_LOGITS);
+    const size_t W = tpw > 0 ? ((size_t)d->T + tpw - 1) / tpw : 0;
+    L.partials = take(W * ((size_t)d->E + 1) * 4);
+  }
   L.act = take(R * (size_t)d->I * 2);
   L.routed = take(R * (size_t)d->H * 2);
   L.total = o;
   L.task_capacity = (int32_t)cap;
   L.token_block = tb;
   L.fast_path = choose_path(d, tb);
-  L.launches = launch_count(d, L.fast_path, tb);
+  L.launches = launch_count(d, L.fast_path, tb, kAssumedCUs);
   return L;
 }
 
@@ -169,6 +184,7 @@ struct moe_plan {
   int num_cus;
   int fuse_router;  // 0: router launch, 1: one token per planner wave, 2: two
   bool planned;     // gate/up routes and plans in its prologue (no planner launch)
+  bool multi;       // multi-workgroup router + planner launch
   int path;
 };
 
@@ -211,11 +227,12 @@ int bind_plan(moe_plan *p, const moe_desc *d) {
   p->path = path;
   p->fuse_router = fuse_router_mode(d);
   p->planned = planned_gate_up(d, path, L.token_block);
-  p->L.launches = launch_count(d, path, L.token_block);
   hipError_t e = hipGetDevice(&p->device);
   if (e == hipSuccess)
     e = hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
   if (e != hipSuccess) return hip_fail(e, "device query");
+  p->multi = multi_planner(d, path, L.token_block, p->num_cus);
+  p->L.launches = launch_count(d, path, L.token_block, p->num_cus);
   return MOE_OK;
 }
 
@@ -316,6 +333,8 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   ra.id64 = d.id_dtype == MOE_IDS_INT64;
   ra.fuse_router = p->fuse_router;
   ra.token_block = L.token_block;
+  ra.partials = (int32_t *)(ws + L.partials);
+  ra.plan_tpw = moe::multi_plan_tokens(d.K, ra.route_logits);
 
   moe::ExpertArgs xa;
   xa.x = (const uint16_t *)d.x;
@@ -344,8 +363,12 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   const bool router = ra.route_logits && !ra.fuse_router;
   int rc = MOE_OK;
   for (int st = first; st < last && rc == MOE_OK; ++st) {
-    // 0 router, 1 plan, 2 gate/up, 3 down, 4 combine, 5 gate/up with the plan
-    const int kind = p->planned ? (st == 0 ? 5 : st + 2) : router ? st : st + 1;
+    // 0 router, 1 plan, 2 gate/up, 3 down, 4 combine, 5 gate/up with the plan,
+    // 6 multi-workgroup router + plan
+    const int kind = p->planned ? (st == 0 ? 5 : st + 2)
+                     : p->multi ? (st == 0 ? 6 : st + 1)
+                     : router   ? st
+                                : st + 1;
     switch (kind) {
       case 0: e = moe::launch_router(ra, s); break;
       case 1: e = moe::launch_route_plan(ra, s); break;
@@ -356,10 +379,12 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
         e = moe::launch_down(xa, L.task_capacity, L.token_block, p->path, p->num_cus, s);
         break;
       case 4: e = moe::launch_combine(xa, s); break;
-      default: e = moe::launch_dma_gate_up_planned(xa, ra, p->num_cus, s); break;
+      case 5: e = moe::launch_dma_gate_up_planned(xa, ra, p->num_cus, s); break;
+      default: e = moe::launch_route_plan_multi(ra, s); break;
     }
     if (e != hipSuccess) {
-      static const char *names[] = {"router", "route plan", "gate/up", "down", "combine", "gate/up"};
+      static const char *names[] = {"router", "route plan", "gate/up", "down", "combine", "gate/up",
+                                    "route plan"};
       rc = hip_fail(e, names[kind]);
     }
   }
@@ -421,7 +446,9 @@ int moe_forward_static(const moe_desc *d, void *stream) {
   // The array keeps the previous call's contents: the work counters and the
   // status words must start at zero.
   e = moe::launch_reset_counters((int32_t *)((char *)ws + L.counters),
-                                 (uint32_t *)((char *)ws + L.status), (hipStream_t)stream);
+                                 (uint32_t *)((char *)ws + L.status),
+                                 (int32_t *)((char *)ws + L.partials),
+                                 (int)((L.act - L.partials) / 4), (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "static workspace reset");
   return run_stages(&p, 0, p.L.launches, stream);
 }
@@ -434,8 +461,10 @@ int moe_plan_reset_counters(moe_plan *p, void *stream) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (prev != p->device && (e = hipSetDevice(p->device)) != hipSuccess)
     return hip_fail(e, "hipSetDevice");
-  e = moe::launch_reset_counters((int32_t *)((char *)p->d.workspace + p->L.counters), nullptr,
-                                 (hipStream_t)stream);
+  char *ws = (char *)p->d.workspace;
+  e = moe::launch_reset_counters((int32_t *)(ws + p->L.counters), nullptr,
+                                 (int32_t *)(ws + p->L.partials),
+                                 (int)((p->L.act - p->L.partials) / 4), (hipStream_t)stream);
   if (prev != p->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(e, "counter reset");
   return MOE_OK;

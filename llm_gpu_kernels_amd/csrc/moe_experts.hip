@@ -199,14 +199,19 @@ hipError_t launch_combine(const ExpertArgs &a, hipStream_t s) {
 }
 
 namespace {
-__global__ void reset_counters_kernel(int32_t *c, uint32_t *status) {
-  if (threadIdx.x < 4) c[threadIdx.x] = 0;
-  if (status && threadIdx.x >= 4 && threadIdx.x < 6) status[threadIdx.x - 4] = 0;
+__global__ void reset_counters_kernel(int32_t *c, uint32_t *status, int32_t *partials, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 4) c[i] = 0;
+  if (status && i >= 4 && i < 6) status[i - 4] = 0;
+  if (i < n) partials[i] = 0;
 }
 }  // namespace
 
-hipError_t launch_reset_counters(int32_t *counters, uint32_t *status, hipStream_t s) {
-  hipLaunchKernelGGL(reset_counters_kernel, dim3(1), dim3(64), 0, s, counters, status);
+hipError_t launch_reset_counters(int32_t *counters, uint32_t *status, int32_t *partials,
+                                 int n_partials, hipStream_t s) {
+  const int blocks = n_partials > 64 ? (n_partials + 255) / 256 : 1;
+  hipLaunchKernelGGL(reset_counters_kernel, dim3(blocks), dim3(256), 0, s, counters, status,
+                     partials, n_partials);
   return hipGetLastError();
 }
 

@@ -17,10 +17,15 @@ struct RouteArgs {
   int4 *tasks;             // {expert, first grouped row, rows, 0}
   int32_t *num_tasks;
   int32_t *counters;       // [4] work counters of the streaming GEMMs
+  int32_t *partials;       // multi-workgroup planner: [W][E + 1] tagged counts and flags
   int T, K, E, R;
   int route_logits, renormalize, id64, fuse_router;
   int token_block;
+  int plan_tpw;            // multi-workgroup planner: tokens per workgroup
 };
+
+// Status bit set when a bounded cross-workgroup wait ran out (never expected).
+constexpr uint32_t kStatusStalled = 16u;
 
 // Expert stage: gate/up + SwiGLU, down projection, weighted combine.
 struct ExpertArgs {
@@ -43,6 +48,10 @@ struct ExpertArgs {
 hipError_t launch_router(const RouteArgs &a, hipStream_t s);
 // Single-workgroup planner (fuses the router when a.fuse_router).
 hipError_t launch_route_plan(const RouteArgs &a, hipStream_t s);
+// Multi-workgroup router + planner (a.plan_tpw tokens per workgroup).
+int multi_plan_tokens(int K, bool router);
+bool multi_plan_ok(int T, int K, bool router, int num_cus);
+hipError_t launch_route_plan_multi(const RouteArgs &a, hipStream_t s);
 
 // token_block: 16 or 32 grouped rows per task.  fast: MFMA kernels (shape
 // constraints checked by the caller), otherwise the generic kernels.
@@ -77,9 +86,11 @@ bool tile_shape_ok(int H, int I, bool w4);
 // Expert-stage kernel families (moe_layout.fast_path).
 enum Path { kGeneric = 0, kStream = 1, kTile = 2 };
 hipError_t launch_combine(const ExpertArgs &a, hipStream_t s);
-// Zero the four work counters (and, when `status` is not null, the two
-// status words) with a kernel: capturable, no memset node.
-hipError_t launch_reset_counters(int32_t *counters, uint32_t *status, hipStream_t s);
+// Zero the four work counters, the planner's `n_partials` published words
+// and, when `status` is not null, the two status words, with a kernel:
+// capturable, no memset node.
+hipError_t launch_reset_counters(int32_t *counters, uint32_t *status, int32_t *partials,
+                                 int n_partials, hipStream_t s);
 hipError_t launch_w4_dequantize(const uint32_t *words_t, const uint16_t *scales_t, int E, int N,
                                 int K, uint16_t *out, hipStream_t s);
 

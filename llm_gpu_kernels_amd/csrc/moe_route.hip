@@ -305,11 +305,277 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
   }
 }
 
+// ---- multi-workgroup router + planner --------------------------------------
+//
+// For every shape the single-workgroup planner does not route itself (T > 32
+// with logits, or any fixed-route shape), one launch of W workgroups routes
+// and plans: workgroup w owns tokens [w*TPW, (w+1)*TPW) (16 tokens, one per
+// wave, with the router; 1024 / K tokens with fixed routes) and
+//  1. routes its tokens (router mode) or loads their ids and weights,
+//  2. ranks its routes canonically within its chunk (wave-ballot match, then
+//     a prefix over its waves) and counts them per expert,
+//  3. publishes its per-expert counts and status bits to the other
+//     workgroups as 32-bit words tagged with this launch's epoch in the high
+//     half (agent-scope stores; the readers re-read a word until its tag is
+//     the epoch, so no fence or barrier orders the exchange),
+//  4. reads every workgroup's counts: base[e] = routes of expert e in earlier
+//     chunks, total[e] = routes of expert e; offsets and task offsets are
+//     exclusive scans of the totals, and rank[q] = base[e] + chunk rank, which
+//     is the canonical rank #{q' < q : id[q'] == e} because chunks are in
+//     route order;
+//  5. writes ranks, map, row_route and row_token of its routes; workgroup 0
+//     also writes counts, offsets, the task list, num_tasks and status, and
+//     finally advances the epoch (every other workgroup read it before
+//     publishing, and workgroup 0 has seen every publication).
+// All W <= CU count workgroups are resident at once (one launch, nothing else
+// on the stream), so every awaited word is being produced; a wait that still
+// exceeds its spin bound sets status bit MOE_STATUS_STALLED instead of hanging.
+constexpr int kMultiThreads = 1024;
+constexpr int kMultiWaves = kMultiThreads / kWave;
+constexpr int kMultiSpinCap = 1 << 20;
+
+__device__ __forceinline__ uint32_t coherent_load(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tag of the epoch value e: never 0, so a zeroed word is never taken as published.
+__device__ __forceinline__ uint32_t epoch_tag(uint32_t e) { return (e & 0x7fffu) | 0x8000u; }
+
+template <typename IdT, bool ROUTER>
+__global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteArgs a) {
+  __shared__ int s_ids[kMultiThreads];
+  __shared__ float s_w[kMultiThreads];
+  __shared__ int s_lrank[kMultiThreads];
+  __shared__ int s_wcnt[kMultiWaves][kMaxExperts];
+  __shared__ int s_base[kMaxExperts], s_tot[kMaxExperts], s_off[kMaxExperts], s_toff[kMaxExperts + 1];
+  __shared__ uint32_t s_flags, s_all_flags;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+  const int E = a.E, K = a.K, W = gridDim.x, w = blockIdx.x;
+  const int tpw = a.plan_tpw;
+  const int t0 = w * tpw, t1 = min(a.T, t0 + tpw);
+  const int q0 = t0 * K, nq = (t1 - t0) * K;  // <= kMultiThreads
+  const uint32_t tag = epoch_tag(coherent_load(a.status + 2));
+  uint32_t *const part = (uint32_t *)a.partials;
+
+  // 1. routes of this chunk into LDS.
+  float raw[4];
+  const int rt = t0 + wave;
+  if (ROUTER) load_token_logits<false>(a.logits, rt, rt < t1, E, raw);
+  if (tid == 0) {
+    s_flags = 0;
+    s_all_flags = 0;
+  }
+  for (int i = tid; i < kMultiWaves * kMaxExperts; i += kMultiThreads) (&s_wcnt[0][0])[i] = 0;
+  uint32_t flags = 0;
+  if constexpr (ROUTER) {
+    if (rt < t1)
+      route_token<false>(raw, rt, true, E, K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
+                         s_ids - q0, s_w - q0);
+  } else {
+    if (tid < nq) {
+      const long long idv = (long long)((const IdT *)a.ids)[q0 + tid];
+      s_ids[tid] = idv >= 0 && idv < E ? (int)idv : -1;
+      s_w[tid] = a.weights[q0 + tid];
+    }
+  }
+  __syncthreads();
+
+  // 2. chunk-local canonical ranks and per-expert counts.
+  const bool valid = tid < nq;
+  const int idv = valid ? s_ids[tid] : -1;
+  const bool ok = idv >= 0;
+  if (valid && !ok) flags |= 1u;
+  if (valid && !isfinite(s_w[tid])) flags |= 2u;
+  const int id = ok ? idv : 0;
+  uint64_t match = __ballot(ok);
+  const int nbits = id_bits(E);
+#pragma unroll
+  for (int bit = 0; bit < 8; ++bit) {
+    if (bit >= nbits) break;
+    const bool set = (id >> bit) & 1;
+    const uint64_t b = __ballot(ok && set);
+    match &= set ? b : ~b;
+  }
+  const int lrank = __popcll(match & lanemask_lt());
+  if (ok && lrank == 0) s_wcnt[wave][id] = __popcll(match);
+  if (flags) atomicOr(&s_flags, flags);
+  __syncthreads();
+  for (int e = tid; e < E; e += kMultiThreads) {
+    int run = 0;
+#pragma unroll
+    for (int v = 0; v < kMultiWaves; ++v) {
+      const int c = s_wcnt[v][e];
+      s_wcnt[v][e] = run;
+      run += c;
+    }
+    // 3. publish the chunk's count of expert e.
+    coherent_store(part + (size_t)w * (E + 1) + e, (tag << 16) | (uint32_t)run);
+  }
+  if (tid == 0) coherent_store(part + (size_t)w * (E + 1) + E, (tag << 16) | s_flags);
+  __syncthreads();
+  if (ok) s_lrank[tid] = s_wcnt[wave][id] + lrank;
+
+  // 4. every chunk's counts.  The W x (E + 1) published words are spread over
+  // the workgroup's threads, eight per request batch: all eight loads are in
+  // flight before any tag is checked (one memory round trip per batch, not
+  // per word), and only a word whose tag has not arrived is read again.
+  // Integer sums, so the order of the LDS additions does not matter.
+  for (int e = tid; e < E; e += kMultiThreads) {
+    s_base[e] = 0;
+    s_tot[e] = 0;
+  }
+  __syncthreads();
+  bool stalled = false;
+  {
+    const int nwords = W * (E + 1);
+    uint32_t fl = 0;
+    for (int j0 = 0; j0 < nwords; j0 += 8 * kMultiThreads) {
+      uint32_t v[8];
+      // The whole batch is re-read (all eight loads in flight again) until
+      // every tag has arrived.
+      for (int n = 0;; ++n) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int j = j0 + i * kMultiThreads + tid;
+          v[i] = j < nwords ? coherent_load(part + j) : (tag << 16);
+        }
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) all &= (v[i] >> 16) == tag;
+        if (all) break;
+        if (n >= kMultiSpinCap) {
+          stalled = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int j = j0 + i * kMultiThreads + tid;
+        if (j >= nwords) continue;
+        const uint32_t c = v[i] & 0xffffu;
+        const int src = j / (E + 1), e = j - src * (E + 1);
+        if (e == E) {
+          fl |= c;
+        } else if (c) {
+          atomicAdd(&s_tot[e], (int)c);
+          if (src < w) atomicAdd(&s_base[e], (int)c);
+        }
+      }
+    }
+    if (stalled) fl |= kStatusStalled;
+    if (fl) atomicOr(&s_all_flags, fl);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int tb = a.token_block;
+    int c[4], nt[4], csum = 0, tsum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane * 4 + j;
+      c[j] = e < E ? s_tot[e] : 0;
+      nt[j] = (c[j] + tb - 1) / tb;
+      csum += c[j];
+      tsum += nt[j];
+    }
+    int crun = wave_incl_scan(csum) - csum, trun = wave_incl_scan(tsum) - tsum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane * 4 + j;
+      if (e < E) {
+        s_off[e] = crun;
+        s_toff[e] = trun;
+        if (w == 0) {
+          a.counts[e] = c[j];
+          a.offsets[e] = crun;
+        }
+      }
+      crun += c[j];
+      trun += nt[j];
+    }
+    if (lane == kWave - 1) s_toff[E] = trun;
+  }
+  __syncthreads();
+
+  // 5. this chunk's rows; workgroup 0 the expert-level arrays.  A workgroup
+  // whose wait ran out writes only the status bit (its counts may be
+  // garbage); if it is workgroup 0 the forward has no tasks.
+  if (s_all_flags & kStatusStalled) {
+    if (tid == 0) {
+      atomicOr(a.status, kStatusStalled);
+      if (w == 0) *a.num_tasks = 0;
+    }
+    return;
+  }
+  if (valid) {
+    const int q = q0 + tid;
+    if (ok) {
+      const int rank = s_base[id] + s_lrank[tid];
+      const int p = s_off[id] + rank;
+      a.ranks[q] = rank;
+      a.map[q] = p;
+      a.row_route[p] = q;
+      a.row_token[p] = q / K;
+    } else {
+      a.ranks[q] = -1;
+      a.map[q] = -1;
+    }
+  }
+  if (w == 0) {
+    const int valid_rows = s_off[E - 1] + s_tot[E - 1];
+    for (int p = valid_rows + tid; p < a.R; p += kMultiThreads) {
+      a.row_route[p] = -1;
+      a.row_token[p] = 0;
+    }
+    const int tb = a.token_block;
+    for (int e = tid; e < E; e += kMultiThreads) {
+      const int c = s_tot[e];
+      int tt = s_toff[e];
+      for (int r0 = 0; r0 < c; r0 += tb, ++tt) a.tasks[tt] = make_int4(e, s_off[e] + r0, min(tb, c - r0), 0);
+    }
+    if (tid == 0) {
+      *a.num_tasks = s_toff[E];
+      a.status[0] = s_all_flags;
+      a.status[1] = 0;
+      a.counters[0] = a.counters[1] = a.counters[2] = a.counters[3] = 0;
+      // Every workgroup read the epoch before publishing, and every
+      // publication has been seen: the next launch may use the next tag.
+      coherent_store(a.status + 2, coherent_load(a.status + 2) + 1u);
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_router(const RouteArgs &a, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
   hipLaunchKernelGGL(router_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+bool multi_plan_ok(int T, int K, bool router, int num_cus) {
+  const int tpw = multi_plan_tokens(K, router);
+  return T > 0 && tpw > 0 && (T + tpw - 1) / tpw <= num_cus && num_cus <= 4096;
+}
+
+int multi_plan_tokens(int K, bool router) {
+  if (router) return K <= kMultiThreads / kMultiWaves ? kMultiWaves : 0;
+  return K <= kMultiThreads ? kMultiThreads / K : 0;
+}
+
+hipError_t launch_route_plan_multi(const RouteArgs &a, hipStream_t s) {
+  const int W = (a.T + a.plan_tpw - 1) / a.plan_tpw;
+  if (W <= 0) return hipSuccess;
+#define MOE_MPLAN(T, R) \
+  hipLaunchKernelGGL((route_plan_multi_kernel<T, R>), dim3(W), dim3(kMultiThreads), 0, s, a)
+  if (a.route_logits) MOE_MPLAN(int32_t, true);
+  else if (a.id64) MOE_MPLAN(long long, false);
+  else MOE_MPLAN(int32_t, false);
+#undef MOE_MPLAN
   return hipGetLastError();
 }
 

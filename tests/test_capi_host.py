@@ -30,13 +30,13 @@ def test_library_exports_every_declared_function():
     assert declared <= set(N.SIGNATURES), declared - set(N.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.moe_abi_version() == 1
+    assert lib.moe_abi_version() == 2
 
 
 def test_struct_sizes_match_header():
-    # 10 int32 + 10 pointers + size_t; 13 size_t + 4 int32.
+    # 10 int32 + 10 pointers + size_t; 14 size_t + 4 int32.
     assert ctypes.sizeof(N.MoeDesc) == 40 + 8 * 10 + 8
-    assert ctypes.sizeof(N.MoeLayout) == 8 * 13 + 16
+    assert ctypes.sizeof(N.MoeLayout) == 8 * 14 + 16
     # 9 int32 (+pad) + 2 + 8 pointers + 8 int64 + float (+pad) + pointer + size_t.
     assert ctypes.sizeof(N.GqaDesc) == 40 + 16 + 64 + 64 + 8 + 8 + 8
 
@@ -72,10 +72,14 @@ def test_layout_for_qwen_shape():
     assert lay.token_block == 32 and lay.fast_path == 1
     rc, lay = _layout(_desc(T=0))
     assert rc == 0 and lay.launches == 0
+    # One multi-workgroup launch routes and plans (16 tokens per workgroup).
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=1024))
-    assert lay.launches == 5
+    assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=193))
-    assert lay.launches == 5
+    assert lay.launches == 4
+    assert lay.partials % 256 == 0 and lay.act >= lay.partials + 13 * 129 * 4
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16 * 256 + 1))
+    assert lay.launches == 5  # more workgroups than CUs: separate router launch
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16))
     assert lay.launches == 3
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17))
@@ -87,9 +91,9 @@ def test_layout_for_qwen_shape():
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, H=4096))
     assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=33))
-    assert lay.launches == 5
+    assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, E=256))
-    assert lay.launches == 5
+    assert lay.launches == 4
     rc, lay = _layout(_desc(H=33, I=19, E=8, K=2))
     assert rc == 0 and lay.fast_path == 0
 
@@ -224,3 +228,9 @@ def test_status_bit_values():
     for name, value in (("BAD_ID", 1), ("BAD_WEIGHT", 2), ("BAD_LOGIT", 4), ("DIRTY_COUNTERS", 8)):
         assert re.search(rf"#define MOE_STATUS_{name} {value}u", text), name
         assert getattr(N, f"STATUS_{name}") == value
+
+
+def test_static_workspace_size_matches_header():
+    text = (INCLUDE / "moe_mi355x.h").read_text()
+    assert re.search(r"#define MOE_STATIC_WORKSPACE_BYTES \(16u << 20\)", text)
+    assert N.STATIC_WORKSPACE_BYTES == 16 << 20

@@ -30,12 +30,12 @@ pytestmark = pytest.mark.gpu
 # (id, T, routing, W4, launches expected, kernel family exercised)
 FAMILIES = [
     ("bf16-t17-planning-gate-up", 17, "uniform", False, 3),   # dma gate/up with routing prologue
-    ("bf16-t193-planner-dma", 193, "uniform", False, 5),      # planner launch + counter-scheduled dma
-    ("bf16-t384-32row-dma", 384, "uniform", False, 5),        # 32-row tasks, 32-row down units in fours
-    ("bf16-t1024-zipf-tiled", 1024, "zipf", False, 5),        # LDS-tiled GEMMs, 64-row tasks
+    ("bf16-t193-planner-dma", 193, "uniform", False, 4),      # multi-workgroup planner + counter-scheduled dma
+    ("bf16-t384-32row-dma", 384, "uniform", False, 4),        # 32-row tasks, 32-row down units in fours
+    ("bf16-t1024-zipf-tiled", 1024, "zipf", False, 4),        # LDS-tiled GEMMs, 64-row tasks
     ("w4-t17-stream", 17, "uniform", True, 4),                # W4 register-streaming gate/up
-    ("w4-t193-wave", 193, "uniform", True, 5),                # W4 one-unit-per-wave gate/up
-    ("w4-t1024-wave", 1024, "uniform", True, 5),              # W4 wave gate/up, 64-row tasks
+    ("w4-t193-wave", 193, "uniform", True, 4),                # W4 one-unit-per-wave gate/up
+    ("w4-t1024-wave", 1024, "uniform", True, 4),              # W4 wave gate/up, 64-row tasks
 ]
 
 _WEIGHTS = {}

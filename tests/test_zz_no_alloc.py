@@ -76,15 +76,27 @@ def test_static_forward_matches_plan(gpu_device):
     assert torch.equal(_bits(out), _bits(expect))
 
 
+def _fits(tokens, route):
+    d = N.MoeDesc()
+    d.T, d.H, d.I, d.E, d.K, d.route_mode = tokens, 2048, 768, 128, 8, route
+    lay = N.MoeLayout()
+    assert N.lib().moe_workspace_layout(ctypes.byref(d), ctypes.byref(lay)) == 0
+    return lay.total <= N.STATIC_WORKSPACE_BYTES
+
+
 def test_static_forward_rejects_large_shapes(gpu_device):
+    """The largest router-mode Qwen-shape forward that fits the static array
+    runs; one token more is rejected with MOE_ESPACE and a message."""
+    limit = max(t for t in range(1, 1024) if _fits(t, N.ROUTE_LOGITS))
+    assert 256 <= limit < 1023
     lay = make_layer("qwen", 1, seed=0, device=gpu_device)
-    inp = make_layer("qwen", 372, seed=1, device=gpu_device, weights=False)
-    ids = torch.zeros((372, 8), dtype=torch.int32, device=gpu_device)
-    w = torch.zeros((372, 8), dtype=torch.float32, device=gpu_device)
-    out = torch.zeros((372, 2048), dtype=torch.bfloat16, device=gpu_device)
+    inp = make_layer("qwen", limit + 1, seed=1, device=gpu_device, weights=False)
+    ids = torch.zeros((limit + 1, 8), dtype=torch.int32, device=gpu_device)
+    w = torch.zeros((limit + 1, 8), dtype=torch.float32, device=gpu_device)
+    out = torch.zeros((limit + 1, 2048), dtype=torch.bfloat16, device=gpu_device)
     d = _desc(inp["x"], lay["down"], ids, w, out, gate_up=lay["gate_up"], logits=inp["logits"])
     assert _static(d) == N.MOE_ESPACE
     assert "static workspace" in N.last_error()
-    d.T = 371
+    d.T = limit
     assert _static(d) == 0, N.last_error()
     torch.cuda.synchronize()
