@@ -119,14 +119,14 @@ def time_layer(plans, steps, warmup):
         tail.replay()
         tail.replay()
     torch.cuda.synchronize()
-    # Keep the GPU busy up to the timed region (an idle gap lets the clocks
-    # drop, and the first timed replays would then run slower than the rest).
-    for i in range(4):
-        rounds[i % 2].replay()
     ev = lambda: torch.cuda.Event(enable_timing=True)
     marks = [ev() for _ in range(replays + 1)]
     end = ev()
     with torch.cuda.stream(stream):
+        # Keep the GPU busy up to the timed region (an idle gap lets the clocks
+        # drop, and the first timed replays would then run slower than the rest).
+        for i in range(4):
+            rounds[i % 2].replay()
         marks[0].record(stream)
         for i in range(replays):
             rounds[i % 2].replay()
