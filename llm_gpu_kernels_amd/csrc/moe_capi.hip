@@ -347,6 +347,8 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   xa.row_route = ra.row_route;
   xa.row_token = ra.row_token;
   xa.num_tasks = ra.num_tasks;
+  xa.counts = ra.counts;
+  xa.offsets = ra.offsets;
   xa.tasks = ra.tasks;
   xa.counters = ra.counters;
   xa.act = (uint16_t *)(ws + L.act);

@@ -36,6 +36,7 @@ struct ExpertArgs {
   const uint16_t *down;        // [E, H, I] bf16
   const float *weights;        // [T, K]
   const int32_t *map, *row_route, *row_token, *num_tasks;
+  const int32_t *counts, *offsets;  // [E] rows per expert and their first grouped row
   const int4 *tasks;
   int32_t *counters;           // [4] {units taken, workgroups done} of gate/up, down
   uint16_t *act;               // [R, I] bf16, grouped-row order
