@@ -231,7 +231,17 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) red[((wave * NRB + rb) * MT + mt) * kWave + lane] = acc[rb][mt];
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (KIND == 0) {
+          // component-major: the epilogue's one-output-per-thread reads are
+          // consecutive floats across lanes (no LDS bank conflicts)
+          float *rf = (float *)red + (((wave * NRB + rb) * MT + mt) * 4) * kWave + lane;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) rf[c * kWave] = acc[rb][mt][c];
+        } else {
+          red[((wave * NRB + rb) * MT + mt) * kWave + lane] = acc[rb][mt];
+        }
+      }
 
     lds_barrier();
 
@@ -246,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
         const int l = et & 63, ii = (et >> 6) & 3, mt = et >> 8;
         const int j = mt * 16 + (l & 15);
         const float *redf = (const float *)red;
-        auto part = [&](int w, int rb) { return redf[(((w * NRB + rb) * MT + mt) * kWave + l) * 4 + ii]; };
+        auto part = [&](int w, int rb) { return redf[((((w * NRB + rb) * MT + mt) * 4 + ii) * kWave + l)]; };
         float sg = part(0, 0), su = part(0, 1);
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) {
