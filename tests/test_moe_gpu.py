@@ -460,3 +460,67 @@ def test_launch_objects_and_workspace_view(gpu_device):
     assert base.mapping.numel() == 193 * 8 and base.down_output.shape == (193 * 8, 2048)
     assert base.workspace_bytes == plan.workspace_bytes
     base.check_inputs()
+
+
+@pytest.mark.parametrize("tokens,k,experts,id_dtype", [(1000, 4, 256, torch.int64),
+                                                       (3000, 1, 7, torch.int32),
+                                                       (2100, 8, 128, torch.int32)])
+def test_multi_workgroup_planner_fixed_routes(tokens, k, experts, id_dtype, gpu_device):
+    """Fixed routes over several planner workgroups (1024 // K tokens each):
+    canonical ranks across chunk boundaries, a hot expert spanning chunks,
+    invalid IDs and a non-finite weight in later chunks (status bits 1 and 2,
+    the bad routes left out of every array), then the same routes made valid
+    through the GEMMs against the FP32 oracle."""
+    g = torch.Generator().manual_seed(tokens + k)
+    ids = torch.randint(0, experts, (tokens, k), generator=g)
+    ids[tokens // 3: tokens // 3 + 300, 0] = 3                    # hot expert across a chunk edge
+    w = torch.rand((tokens, k), generator=g)
+    x = torch.randn((tokens, 128), generator=g).to(torch.bfloat16)
+    gu = (torch.randn((experts, 256, 128), generator=g) * 0.05).to(torch.bfloat16)
+    dn = (torch.randn((experts, 128, 128), generator=g) * 0.05).to(torch.bfloat16)
+    bad = ids.clone()
+    bad[tokens - 5, k - 1] = experts                                # invalid, last chunk
+    bad[tokens // 2, 0] = -1                                        # invalid, middle chunk
+    wbad = w.clone()
+    wbad[tokens - 700, 0] = float("nan")
+    dev = _to(gpu_device, x, gu, dn, bad.to(id_dtype), wbad)
+    plan = prepare_moe(*dev)
+    assert plan.launch_names[0] == "route_plan"
+    torch.cuda.synchronize()
+    assert plan.read_status() == 3
+    _check_dispatch(plan, bad, experts)
+    # valid routes: dispatch and layer output
+    plan.ids.copy_(ids.to(id_dtype).to(gpu_device))
+    plan.routing_weights.copy_(w.to(gpu_device))
+    out = plan.run().clone()
+    torch.cuda.synchronize()
+    assert plan.read_status() == 0
+    _check_dispatch(plan, ids, experts)
+    m = O.error(out, O.moe_reference(x, gu, dn, ids, w))
+    assert m["passed"], m
+
+
+def test_multi_workgroup_router(gpu_device):
+    """Router mode above 32 tokens with E = 256 (no single-workgroup fusion):
+    38 planner workgroups route 16 tokens each; IDs bit-exact on tie-heavy
+    logits, the dispatch canonical, a NaN logit in the last chunk sets bit 4."""
+    tokens, experts, k = 600, 256, 6
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn((tokens, 128), generator=g).to(torch.bfloat16)
+    gu = (torch.randn((experts, 256, 128), generator=g) * 0.05).to(torch.bfloat16)
+    dn = (torch.randn((experts, 128, 128), generator=g) * 0.05).to(torch.bfloat16)
+    logits = torch.randint(-5, 5, (tokens, experts), generator=g).float() * 0.5
+    plan = prepare_routed_moe(*_to(gpu_device, x, logits, gu, dn), k)
+    assert plan.launch_names[0] == "route_plan"
+    out = plan.forward().clone()
+    torch.cuda.synchronize()
+    ids, w = O.route_topk(logits, k)
+    assert torch.equal(plan.ids.cpu(), ids), "router IDs differ"
+    assert torch.allclose(plan.routing_weights.cpu(), w, rtol=2e-6, atol=1e-7)
+    _check_dispatch(plan, ids, experts)
+    assert plan.read_status() == 0
+    m = O.error(out, O.moe_reference(x, gu, dn, ids, w))
+    assert m["passed"], m
+    plan.logits[tokens - 3, 17] = float("nan")
+    plan.forward()
+    assert plan.read_status() & 4
