@@ -9,11 +9,11 @@
 //   are fp32, probabilities are rounded to bf16 for the P.V product (as the
 //   reference does), the output is bf16.
 //
-// Design.  A workgroup of four waves owns 64 query rows of one KV head: four
-// 16-row blocks, each one query head x 16 tokens (HPW heads x 64/HPW tokens).
-// The waves split the workgroup's visible keys into four contiguous ranges and
-// each wave runs its own online softmax over all 64 rows, 32 keys per step,
-// with no workgroup barrier in the loop:
+// Design.  A workgroup of four or eight waves owns 16 * RB query rows of one
+// KV head (RB = 2: two 16-row blocks, each one query head x 16 tokens).  The
+// waves split the workgroup's visible keys into contiguous ranges and each
+// wave runs its own online softmax over all of the workgroup's rows, 32 keys
+// per step, with no workgroup barrier in the loop:
 //   * scores are computed transposed, S^T = K Q^T, with 16x16x32 bf16 MFMAs;
 //     K fragments (A operand) are loaded from HBM straight into registers,
 //     Q fragments (B operand) stay in registers for the whole kernel, and the
@@ -24,10 +24,10 @@
 //     yields the B operand (8 keys x 1 dim per lane) directly;
 //   * the next step's K and V are prefetched into registers while the current
 //     step computes.
-// At the end the four waves' (max, sum, O) states are merged in LDS in fixed
-// wave order.  When there are too few workgroups to fill the chip the keys
-// are also split across workgroups and a second kernel merges the partial
-// states in fixed split order.
+// At the end the waves' (max, sum, O) states are merged in LDS in fixed wave
+// order.  When there are too few workgroups to fill the chip the keys are
+// also split across workgroups and a second kernel merges the partial states
+// in fixed split order (gqa_shape).
 #include <climits>
 #include "common.h"
 #include "gqa_internal.h"
@@ -37,7 +37,6 @@ namespace moe {
 namespace {
 
 constexpr int kD = 128;      // head_dim
-constexpr int kWaves = 4;    // waves per workgroup
 constexpr int kKC = 32;      // keys per wave step
 constexpr int kMaxSplits = 16;
 #ifndef GQA_ROW_BLOCKS
@@ -119,15 +118,17 @@ __device__ __forceinline__ int xcd_logical_block(int id, int n) {
 }
 
 // RB 16-row blocks per wave; HPW query heads per workgroup (HPW divides RB);
-// row block rb is (head rb % HPW, token block rb / HPW).  With RB = 2 the
-// kernel fits two workgroups per CU (two waves per SIMD).
-template <int RB, int HPW>
-__global__ __launch_bounds__(64 * kWaves, 4 / RB) void gqa_fwd_kernel(GqaArgs a, int head_groups,
-                                                                      int nqb, int nsplit) {
+// row block rb is (head rb % HPW, token block rb / HPW); NW waves split the
+// workgroup's keys.  With RB = 2 the kernel keeps two waves per SIMD: two
+// four-wave workgroups or one eight-wave workgroup per CU.
+template <int RB, int HPW, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(GqaArgs a, int head_groups,
+                                                                               int nqb, int nsplit) {
+  constexpr int kWaves = NW;
   constexpr int kRB = RB;
   constexpr int QT = 16 * (kRB / HPW);                 // tokens per workgroup
   constexpr int kStage = kKC * kD * 2;                 // V staging per wave (8 KB)
-  constexpr int kOBytes = kWaves * kRB * 8 * 64 * 16;  // merge: O states (32 KB per row block)
+  constexpr int kOBytes = kWaves * kRB * 8 * 64 * 16;  // merge: O states (8 KB per wave and row block)
   constexpr int kMLBytes = kWaves * kRB * 16 * 2 * 4;  // merge: (m, l) per row
   static_assert(kWaves * kStage <= kOBytes, "V staging aliases the merge area");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kOBytes + kMLBytes];
@@ -299,13 +300,14 @@ __global__ __launch_bounds__(64 * kWaves, 4 / RB) void gqa_fwd_kernel(GqaArgs a,
       }
       // The scale is positive, so the maximum is taken on raw scores and the
       // scale is folded into the exponent's FMA (base-2 domain).
-      float tmax = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
-                         fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3])));
-      tmax = rows_max(tmax) * sl2;
+      const float lmax = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
+                               fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3]))) * sl2;
       // Rescale only when some row's maximum outgrows the slack (wave-uniform
-      // branch).  A row with no visible key so far keeps m = -inf.
-      if (__builtin_amdgcn_ballot_w64(tmax > m_run[rb] + kRescaleSlack)) {
-        const float m_new = fmaxf(m_run[rb], tmax);
+      // branch).  A row's maximum exceeds m + slack exactly when one of its
+      // four lanes' maxima does, so the cross-lane maximum is only taken on
+      // this rare path.  A row with no visible key so far keeps m = -inf.
+      if (__builtin_amdgcn_ballot_w64(lmax > m_run[rb] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[rb], rows_max(lmax));
         const float alpha = __builtin_amdgcn_exp2f(m_run[rb] - (m_new == -INFINITY ? 0.f : m_new));
         l_run[rb] *= alpha;
         m_run[rb] = m_new;
@@ -318,19 +320,17 @@ __global__ __launch_bounds__(64 * kWaves, 4 / RB) void gqa_fwd_kernel(GqaArgs a,
           for (int i = 0; i < 4; ++i) o[rb][dt][i] *= al[i];
       }
       const float neg_m = m_run[rb] == -INFINITY ? 0.f : -m_run[rb];
-      float psum = 0.f;
       float p[2][4];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][kt][i], sl2, neg_m));
-          psum += p[kt][i];
-        }
+        for (int i = 0; i < 4; ++i) p[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][kt][i], sl2, neg_m));
+      // l is kept per lane (the lane's keys only) and summed over the row's
+      // four lanes once, after the loop; alpha is the same on all four.
+      l_run[rb] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
       // A operand of P.V: slots 0..3 = keys 4g + i, slots 4..7 = keys 16 + 4g + i.
       const u32x4 pa = u32x4{pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
                              pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
-      l_run[rb] += rows_sum(psum);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) o[rb][dt] = mfma16(pa, vb[dt], o[rb][dt]);
     }
@@ -338,7 +338,10 @@ __global__ __launch_bounds__(64 * kWaves, 4 / RB) void gqa_fwd_kernel(GqaArgs a,
     cur = nxt;
   }
 
-  // Merge of the four waves' states, fixed wave order.  The staging areas
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) l_run[rb] = rows_sum(l_run[rb]);
+
+  // Merge of the waves' states, fixed wave order.  The staging areas
   // are reused, so every wave must be past its loop first.
   float *ost = (float *)smem;               // [wave][rb][dt][lane] x 4
   float *ml = (float *)(smem + kOBytes);    // [wave][rb][row] x {m, l}
@@ -351,8 +354,9 @@ __global__ __launch_bounds__(64 * kWaves, 4 / RB) void gqa_fwd_kernel(GqaArgs a,
   }
   __syncthreads();
 
-  // Wave w finalises row block w % RB, dims 64 * (w / RB) .. +64 when RB = 2
-  // (all 128 dims when RB = 4): lane holds tokens 4g + i, dims 16dt + r.
+  // Wave w finalises row block w % RB, dims 16 kDT (w / RB) .. + 16 kDT (64
+  // dims per wave with four waves and RB = 2, 32 with eight): lane holds
+  // tokens 4g + i, dims 16dt + r.
   static_assert(kWaves % kRB == 0, "row blocks are shared out evenly over the waves");
   constexpr int kDT = 8 * kRB / kWaves;  // 16-dim column tiles per finalising wave
   const int rb = wave % kRB, dt0 = (wave / kRB) * kDT;
@@ -455,37 +459,61 @@ __global__ __launch_bounds__(128) void gqa_merge_kernel(GqaArgs a, int nsplit) {
 constexpr int kLaunchRB = GQA_ROW_BLOCKS;
 int gqa_heads_per_wg(int G) { return G < kLaunchRB ? G : kLaunchRB; }
 
-int gqa_num_splits(int T, int Hq, int Hkv, int num_cus) {
+// Workgroups (of either width) cover 16 * RB query rows each.  With enough of
+// them for two per CU: four-wave workgroups, no split.  Otherwise eight-wave
+// workgroups, one per CU (the same two waves per SIMD, keys split eight ways
+// inside the workgroup and merged in LDS), and the keys are split across
+// workgroups only as many times as fills the CUs without starting a second,
+// partial round of workgroups (rounding the split count up measured 5 us
+// slower at T = 96); with one workgroup per CU or more there is no merge
+// launch at all.
+GqaShape gqa_shape(int T, int Hq, int Hkv, int num_cus) {
   const int G = Hq / Hkv, hpw = gqa_heads_per_wg(G);
   const int qt = 16 * (kLaunchRB / hpw);
   const int wgs = ((T + qt - 1) / qt) * Hkv * (G / hpw);
-  if (wgs <= 0) return 1;
-  const int per_cu = 4 / kLaunchRB;  // resident workgroups per CU
-  int s = (num_cus * per_cu + wgs - 1) / wgs;
+  if (wgs <= 0) return {1, 4};
+  const int per_cu = 4 / kLaunchRB;  // resident four-wave workgroups per CU
+  if (wgs >= num_cus * per_cu) return {1, 4};
+  const int waves = kLaunchRB == 2 ? 8 : 4;
+  const int slots = waves == 8 ? num_cus : num_cus * per_cu;
+  int s = slots / wgs;
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
-  return s;
+  return {s, waves};
 }
 
 size_t gqa_partial_bytes(int T, int Hq, int nsplit) {
   return nsplit > 1 ? (size_t)nsplit * T * Hq * (kD + 2) * sizeof(float) : 0;
 }
 
-hipError_t launch_gqa(const GqaArgs &a, int nsplit, hipStream_t s) {
+template <int NW>
+hipError_t launch_fwd(const GqaArgs &a, int hpw, dim3 grid, int groups, int nqb, int nsplit,
+                      hipStream_t s) {
+  const dim3 block(64 * NW);
+  switch (hpw) {
+    case 1: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 1, NW>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+    case 2: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 2, NW>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+#if GQA_ROW_BLOCKS == 4
+    case 4: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 4, NW>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+#endif
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gqa(const GqaArgs &a, GqaShape shape, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
   const int G = a.Hq / a.Hkv, hpw = gqa_heads_per_wg(G);
   const int qt = 16 * (kLaunchRB / hpw), groups = G / hpw;
   const int nqb = (a.T + qt - 1) / qt;
-  const dim3 grid(nqb * a.Hkv * groups * nsplit), block(64 * kWaves);
-  switch (hpw) {
-    case 1: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 1>), grid, block, 0, s, a, groups, nqb, nsplit); break;
-    case 2: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 2>), grid, block, 0, s, a, groups, nqb, nsplit); break;
-#if GQA_ROW_BLOCKS == 4
-    case 4: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 4>), grid, block, 0, s, a, groups, nqb, nsplit); break;
+  const int nsplit = shape.nsplit;
+  const dim3 grid(nqb * a.Hkv * groups * nsplit);
+  hipError_t e;
+#if GQA_ROW_BLOCKS == 2
+  if (shape.waves == 8) e = launch_fwd<8>(a, hpw, grid, groups, nqb, nsplit, s);
+  else
 #endif
-    default: return hipErrorInvalidValue;
-  }
-  hipError_t e = hipGetLastError();
+    e = launch_fwd<4>(a, hpw, grid, groups, nqb, nsplit, s);
   if (e != hipSuccess || nsplit == 1) return e;
   hipLaunchKernelGGL(gqa_merge_kernel, dim3(a.T * a.Hq), dim3(kD), 0, s, a, nsplit);
   return hipGetLastError();

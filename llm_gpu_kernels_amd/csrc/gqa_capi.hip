@@ -19,7 +19,7 @@ int capi_fail(int code, const char *fmt, ...);  // moe_capi.hip (thread-local me
 
 struct gqa_seg_plan {
   moe::GqaArgs a;
-  int nsplit;
+  moe::GqaShape shape;
   int device;
 };
 
@@ -29,7 +29,7 @@ constexpr int64_t kMaxTokenStride = 1LL << 25;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-int validate(const gqa_seg_desc *d, int num_cus, int *nsplit) {
+int validate(const gqa_seg_desc *d, int num_cus, moe::GqaShape *shape) {
   using moe::capi_fail;
   if (!d) return capi_fail(MOE_EINVAL, "null descriptor");
   if (d->D != 128) return capi_fail(MOE_EINVAL, "head_dim must be 128 (got %d)", d->D);
@@ -62,7 +62,7 @@ int validate(const gqa_seg_desc *d, int num_cus, int *nsplit) {
     return capi_fail(MOE_EINVAL, "q/out must be non-null and 16-byte aligned");
   if ((long long)d->T * d->Hq * 128 >= (1LL << 31))
     return capi_fail(MOE_EINVAL, "T * Hq * 128 must be < 2^31");
-  *nsplit = moe::gqa_num_splits(d->T, d->Hq, d->Hkv, num_cus);
+  *shape = moe::gqa_shape(d->T, d->Hq, d->Hkv, num_cus);
   return MOE_OK;
 }
 
@@ -78,23 +78,25 @@ int device_cus(int *device, int *cus) {
 extern "C" {
 
 int gqa_seg_workspace_bytes(const gqa_seg_desc *d, size_t *bytes) {
-  int dev = 0, cus = 0, ns = 1;
+  int dev = 0, cus = 0;
+  moe::GqaShape shape{1, 4};
   int rc = device_cus(&dev, &cus);
   if (rc) return rc;
-  if ((rc = validate(d, cus, &ns))) return rc;
+  if ((rc = validate(d, cus, &shape))) return rc;
   if (!bytes) return moe::capi_fail(MOE_EINVAL, "null bytes");
-  *bytes = moe::gqa_partial_bytes(d->T, d->Hq, ns);
+  *bytes = moe::gqa_partial_bytes(d->T, d->Hq, shape.nsplit);
   return MOE_OK;
 }
 
 int gqa_seg_plan_create(gqa_seg_plan **out, const gqa_seg_desc *d) {
   if (!out) return moe::capi_fail(MOE_EINVAL, "null plan pointer");
   *out = nullptr;
-  int dev = 0, cus = 0, ns = 1;
+  int dev = 0, cus = 0;
+  moe::GqaShape shape{1, 4};
   int rc = device_cus(&dev, &cus);
   if (rc) return rc;
-  if ((rc = validate(d, cus, &ns))) return rc;
-  const size_t need = moe::gqa_partial_bytes(d->T, d->Hq, ns);
+  if ((rc = validate(d, cus, &shape))) return rc;
+  const size_t need = moe::gqa_partial_bytes(d->T, d->Hq, shape.nsplit);
   if (need && (d->workspace_bytes < need || !d->workspace || !aligned16(d->workspace)))
     return moe::capi_fail(MOE_ESPACE, "workspace has %zu bytes, needs %zu", d->workspace_bytes,
                           need);
@@ -119,7 +121,7 @@ int gqa_seg_plan_create(gqa_seg_plan **out, const gqa_seg_desc *d) {
   a.Hkv = d->Hkv;
   a.scale = (d->scale > 0.f && d->scale < INFINITY) ? d->scale : 1.0f / sqrtf((float)d->D);
   a.partial = (float *)d->workspace;
-  p->nsplit = ns;
+  p->shape = shape;
   p->device = dev;
   *out = p;
   return MOE_OK;
@@ -131,7 +133,7 @@ int gqa_seg_plan_run(gqa_seg_plan *p, void *stream) {
   int prev = -1;
   hipError_t e = hipGetDevice(&prev);
   if (e == hipSuccess && prev != p->device) e = hipSetDevice(p->device);
-  if (e == hipSuccess) e = moe::launch_gqa(p->a, p->nsplit, (hipStream_t)stream);
+  if (e == hipSuccess) e = moe::launch_gqa(p->a, p->shape, (hipStream_t)stream);
   if (prev >= 0 && prev != p->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return moe::capi_fail(MOE_EDEVICE, "gqa launch: %s", hipGetErrorString(e));
   return MOE_OK;

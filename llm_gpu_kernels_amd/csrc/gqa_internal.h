@@ -22,8 +22,14 @@ struct GqaArgs {
   float *partial;                        // split-K partial states (nsplit > 1)
 };
 
-int gqa_num_splits(int T, int Hq, int Hkv, int num_cus);
+// Launch shape: key splits across workgroups (merged by a second kernel when
+// > 1) and waves per workgroup (4 or 8).
+struct GqaShape {
+  int nsplit;
+  int waves;
+};
+GqaShape gqa_shape(int T, int Hq, int Hkv, int num_cus);
 size_t gqa_partial_bytes(int T, int Hq, int nsplit);
-hipError_t launch_gqa(const GqaArgs &a, int nsplit, hipStream_t s);
+hipError_t launch_gqa(const GqaArgs &a, GqaShape shape, hipStream_t s);
 
 }  // namespace moe

@@ -45,6 +45,17 @@ def test_baseline_config5(tokens, gpu_device):
     _check(plan.output, q, segs)
 
 
+@pytest.mark.parametrize("tokens", [200, 512])
+def test_launch_shapes(tokens, gpu_device):
+    """The other launch shapes on 256 CUs: T = 200 runs eight-wave workgroups
+    without a split (fewer workgroups than CUs, no merge launch); T = 512 runs
+    four-wave workgroups, two per CU, without a split."""
+    q, segs = _values(tokens + 1, tokens, (300, 0, 129), gpu_device)
+    plan = prepare_segmented_gqa(q, segs)
+    torch.cuda.synchronize()
+    _check(plan.output, q, segs)
+
+
 @pytest.mark.parametrize("tokens,history", [(96, (2049, 0, 575)), (17, (0, 0, 0)), (1, (5, 0, 3)),
                                             (33, (64, 63, 1))])
 def test_reference_shapes_and_tails(tokens, history, gpu_device):
