@@ -286,11 +286,11 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
     }
 
     const bool full = cur.n == kKC && !cur.causal;
+    // Mask (raw scores): rows past the step's end and, in the current
+    // segment, keys after the token (key j of the current chunk is token j).
+    if (!full) {
 #pragma unroll
-    for (int rb = 0; rb < kRB; ++rb) {
-      // Mask (raw scores): rows past the step's end and, in the current
-      // segment, keys after the token (key j of the current chunk is token j).
-      if (!full) {
+      for (int rb = 0; rb < kRB; ++rb) {
         const int tok = q0 + 16 * (rb / HPW) + r;
         const int lim = cur.causal ? min(cur.n - 1, tok - cur.local0) : cur.n - 1;
 #pragma unroll
@@ -298,16 +298,29 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) s[rb][kt][i] = 16 * kt + 4 * g + i <= lim ? s[rb][kt][i] : -INFINITY;
       }
-      // The scale is positive, so the maximum is taken on raw scores and the
-      // scale is folded into the exponent's FMA (base-2 domain).
-      const float lmax = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
-                               fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3]))) * sl2;
-      // Rescale only when some row's maximum outgrows the slack (wave-uniform
-      // branch).  A row's maximum exceeds m + slack exactly when one of its
-      // four lanes' maxima does, so the cross-lane maximum is only taken on
-      // this rare path.  A row with no visible key so far keeps m = -inf.
-      if (__builtin_amdgcn_ballot_w64(lmax > m_run[rb] + kRescaleSlack)) {
-        const float m_new = fmaxf(m_run[rb], rows_max(lmax));
+    }
+    // The row blocks' softmax chains are independent: every stage below runs
+    // over all of them before the next, so their dependent instructions
+    // interleave.  The scale is positive, so the maximum is taken on raw
+    // scores and the scale is folded into the exponent's FMA (base-2 domain).
+    float lmax[kRB];
+    bool grow = false;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      lmax[rb] = fmaxf(fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), fmaxf(s[rb][0][2], s[rb][0][3])),
+                       fmaxf(fmaxf(s[rb][1][0], s[rb][1][1]), fmaxf(s[rb][1][2], s[rb][1][3]))) * sl2;
+      grow |= lmax[rb] > m_run[rb] + kRescaleSlack;
+    }
+    // Rescale only when some row's maximum outgrows the slack (one
+    // wave-uniform branch for all row blocks).  A row's maximum exceeds
+    // m + slack exactly when one of its four lanes' maxima does, so the
+    // cross-lane maximum is only taken on this rare path; rows that did not
+    // grow get alpha = 1 exactly.  A row with no visible key so far keeps
+    // m = -inf.
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) {
+        const float m_new = fmaxf(m_run[rb], rows_max(lmax[rb]));
         const float alpha = __builtin_amdgcn_exp2f(m_run[rb] - (m_new == -INFINITY ? 0.f : m_new));
         l_run[rb] *= alpha;
         m_run[rb] = m_new;
@@ -319,6 +332,10 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[rb][dt][i] *= al[i];
       }
+    }
+    u32x4 pa[kRB];
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
       const float neg_m = m_run[rb] == -INFINITY ? 0.f : -m_run[rb];
       float p[2][4];
 #pragma unroll
@@ -329,11 +346,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
       // four lanes once, after the loop; alpha is the same on all four.
       l_run[rb] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
       // A operand of P.V: slots 0..3 = keys 4g + i, slots 4..7 = keys 16 + 4g + i.
-      const u32x4 pa = u32x4{pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
-                             pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[rb][dt] = mfma16(pa, vb[dt], o[rb][dt]);
+      pa[rb] = u32x4{pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                     pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
     }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) o[rb][dt] = mfma16(pa[rb], vb[dt], o[rb][dt]);
     pos = next;
     cur = nxt;
   }
