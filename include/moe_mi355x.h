@@ -51,7 +51,8 @@ extern "C" {
 
 /* moe_desc.weight_format */
 #define MOE_WEIGHTS_BF16 0        /* gate_up bf16 [E, 2I, H]                  */
-#define MOE_WEIGHTS_W4G128 1      /* gate_up int4 in the tiled layout below   */
+#define MOE_WEIGHTS_W4G128 1      /* gate_up int4 in the tiled layout below;  *
+                                   * needs H % 128 == 0 and I % 32 == 0        */
 
 /* moe_desc.id_dtype */
 #define MOE_IDS_INT32 0
@@ -107,7 +108,8 @@ typedef struct moe_layout {
                        * (T <= 32); 5 (separate router launch) only for shapes   *
                        * with more tokens than the planner's workgroups hold     *
                        * (T > 16 x CU count); 0 when T == 0                      */
-  int32_t fast_path;  /* 0 generic kernels (unaligned shapes), 1 MFMA weight      
+  int32_t fast_path;  /* 0 run-time-K MFMA kernels (other shapes; scalar where   
+                         H or I is not a multiple of 32), 1 MFMA weight         
                          streaming, 2 MFMA LDS-tiled (many rows per expert)     */
 } moe_layout;
 

@@ -70,8 +70,6 @@ int choose_path(const moe_desc *d, int tb) {
   return moe::stream_shape_ok(d->H, d->I, w4) ? moe::kStream : moe::kGeneric;
 }
 
-bool shape_fast(const moe_desc *d, int tb) { return choose_path(d, tb) != moe::kGeneric; }
-
 int validate(const moe_desc *d) {
   if (!d) return fail(MOE_EINVAL, "null descriptor");
   if (d->E < 1 || d->E > 256) return fail(MOE_EINVAL, "E must be in [1, 256] (got %d)", d->E);
@@ -96,8 +94,8 @@ int validate(const moe_desc *d) {
       d->token_block != 64)
     return fail(MOE_EINVAL, "token_block must be 0, 16, 32 or 64");
   if (d->weight_format == MOE_WEIGHTS_W4G128) {
-    if (!shape_fast(d, choose_token_block(d)))
-      return fail(MOE_EINVAL, "W4G128 needs H %% 1024 == 0, I %% 256 == 0, H, I <= 4096");
+    if (!moe::flex_shape_ok(d->H, d->I, true))
+      return fail(MOE_EINVAL, "W4G128 needs H %% 128 == 0 and I %% 32 == 0");
   }
   return MOE_OK;
 }
@@ -212,18 +210,18 @@ int bind_plan(moe_plan *p, const moe_desc *d) {
   }
   int path = L.fast_path;
   // A stream-sized task block on a shape only the tiled kernels take (or the
-  // reverse) cannot happen: choose_path already matched them.
-  bool fast = path != moe::kGeneric;
-  if (fast && !(aligned16(d->x) && aligned16(d->down) && aligned16(d->out) &&
-                (d->weight_format == MOE_WEIGHTS_W4G128 ? aligned16(d->w4_words)
-                                                        : aligned16(d->gate_up))))
-    fast = false;
-  if (!fast) path = moe::kGeneric;
-  if (!fast && d->weight_format == MOE_WEIGHTS_W4G128)
+  // reverse) cannot happen: choose_path already matched them.  Every MFMA
+  // kernel (tuned or run-time-K) reads 16-byte fragments: with an unaligned
+  // buffer a bf16 forward takes the scalar kernels.
+  const bool aligned = aligned16(d->x) && aligned16(d->down) && aligned16(d->out) &&
+                       (d->weight_format == MOE_WEIGHTS_W4G128 ? aligned16(d->w4_words)
+                                                               : aligned16(d->gate_up));
+  if (!aligned && d->weight_format == MOE_WEIGHTS_W4G128)
     return fail(MOE_EINVAL, "W4G128 buffers must be 16-byte aligned");
+  if (!aligned) path = moe::kScalar;
   p->d = *d;
   p->L = L;
-  p->L.fast_path = path;
+  p->L.fast_path = path == moe::kScalar ? moe::kGeneric : path;
   p->path = path;
   p->fuse_router = fuse_router_mode(d);
   p->planned = planned_gate_up(d, path, L.token_block);

@@ -160,8 +160,8 @@ hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_bloc
   // W4 with several rows per expert, and every 64-row task: decode each weight
   // fragment once for up to 64 token rows (one unit per wave).  With about one
   // row per expert the split-K streaming kernel overlaps the decode better.
-  if (w4 && path != kGeneric && (token_block == 64 || (long long)a.R >= 4LL * a.E) &&
-      wave_w4_shape_ok(a.H, a.I, token_block))
+  const bool wave_ok = w4 && wave_w4_shape_ok(a.H, a.I, token_block);
+  if (wave_ok && path != kGeneric && (token_block == 64 || (long long)a.R >= 4LL * a.E))
     return launch_wave_w4_gate_up(a, task_capacity, token_block, s);
   if (path == kTile) return w4 ? hipErrorInvalidValue : launch_tile_gate_up(a, task_capacity, num_cus, s);
   if (path == kStream) {
@@ -169,6 +169,12 @@ hipError_t launch_gate_up(const ExpertArgs &a, int task_capacity, int token_bloc
       return launch_dma_gate_up(a, token_block, num_cus, s);
     return launch_stream_gate_up(a, task_capacity, token_block, w4, num_cus, s);
   }
+  // Shapes the tuned kernels do not take: the W4 wave kernel where its K-chunks
+  // fit, else the run-time-K MFMA kernel, else (bf16, H or I not a multiple of
+  // 32) the scalar one.
+  if (wave_ok) return launch_wave_w4_gate_up(a, task_capacity, token_block, s);
+  if (path == kGeneric && flex_shape_ok(a.H, a.I, w4))
+    return launch_flex_gate_up(a, task_capacity, token_block, w4, s);
   if (w4) return hipErrorInvalidValue;
   const dim3 grid(task_capacity, (token_block * a.I + 255) / 256);
   hipLaunchKernelGGL(gate_up_generic_kernel, grid, dim3(256), 0, s, a, token_block);
@@ -182,6 +188,8 @@ hipError_t launch_down(const ExpertArgs &a, int task_capacity, int token_block, 
     if (kDmaStreaming && kDmaDown && dma_shape_ok(a.H, a.I, token_block)) return launch_dma_down(a, token_block, num_cus, s);
     return launch_stream_down(a, task_capacity, token_block, num_cus, s);
   }
+  if (path == kGeneric && flex_shape_ok(a.H, a.I, false))
+    return launch_flex_down(a, task_capacity, token_block, s);
   const dim3 grid(task_capacity, (token_block * a.H + 255) / 256);
   hipLaunchKernelGGL(down_generic_kernel, grid, dim3(256), 0, s, a, token_block);
   return hipGetLastError();

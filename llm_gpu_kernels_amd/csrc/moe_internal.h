@@ -85,7 +85,15 @@ hipError_t launch_tile_down(const ExpertArgs &a, int task_capacity, int num_cus,
 bool tile_shape_ok(int H, int I, bool w4);
 
 // Expert-stage kernel families (moe_layout.fast_path).
-enum Path { kGeneric = 0, kStream = 1, kTile = 2 };
+// kGeneric: the run-time-K MFMA kernels (or scalar kernels where H or I is not
+// a multiple of 32); kScalar: the scalar kernels (unaligned bf16 buffers).
+enum Path { kGeneric = 0, kStream = 1, kTile = 2, kScalar = 3 };
+// MFMA kernels for any H, I that are multiples of 32 (W4: H of 128) -- the
+// shapes the tuned kernels above do not take (kGeneric path).
+bool flex_shape_ok(int H, int I, bool w4);
+hipError_t launch_flex_gate_up(const ExpertArgs &a, int task_capacity, int token_block, bool w4,
+                               hipStream_t s);
+hipError_t launch_flex_down(const ExpertArgs &a, int task_capacity, int token_block, hipStream_t s);
 hipError_t launch_combine(const ExpertArgs &a, hipStream_t s);
 // Zero the four work counters, the planner's `n_partials` published words
 // and, when `status` is not null, the two status words, with a kernel:

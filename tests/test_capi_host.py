@@ -102,7 +102,7 @@ def test_layout_for_qwen_shape():
                                 dict(I=-1), dict(T=-1), dict(fmt=7), dict(ids=9), dict(tb=8), dict(tb=48),
                                 dict(route=N.ROUTE_LOGITS, ids=N.IDS_INT64),
                                 dict(route=N.ROUTE_LOGITS, E=4, K=8),
-                                dict(fmt=N.WEIGHTS_W4G128, H=192), dict(fmt=N.WEIGHTS_W4G128, H=512, I=256),
+                                dict(fmt=N.WEIGHTS_W4G128, H=192), dict(fmt=N.WEIGHTS_W4G128, H=512, I=48),
                                 dict(T=2 ** 27, K=16)])
 def test_layout_rejects_invalid_descriptors(kw):
     rc, _ = _layout(_desc(**kw))

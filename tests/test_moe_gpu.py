@@ -184,6 +184,47 @@ def test_w4_token_blocks(tokens, gpu_device):
         assert m["passed"], (bm, m)
 
 
+# (tokens, experts, topk, H, I, W4): shapes outside the tuned kernels' compile-time K
+# steps -- GPT-OSS-like H = 2880, DeepSeek-like H = 7168, H/I = 1056/608, W4 H = 1152 and
+# 4096 -- through each run-time-K MFMA kernel (16/32/64-row tasks, bf16 and W4) and
+# the W4 wave kernel taking a shape the split-K streaming kernel cannot.
+FLEX_SHAPES = [
+    (17, 8, 4, 2880, 1440, False),   # 16-row tasks
+    (100, 8, 2, 2880, 1440, False),  # 32-row tasks
+    (300, 8, 2, 1056, 608, False),   # 64-row tasks, I % 128 != 0
+    (5, 4, 2, 7168, 512, False),
+    (17, 8, 4, 4096, 512, True),     # W4: wave kernel gate/up, run-time-K down
+    (9, 8, 2, 1152, 384, True),      # W4 run-time-K gate/up, 16-row tasks
+    (100, 8, 2, 1152, 384, True),    # 32-row tasks
+    (300, 8, 2, 1152, 384, True),    # 64-row tasks
+]
+
+
+@pytest.mark.parametrize("tokens,experts,topk,hidden,inter,w4", FLEX_SHAPES,
+                         ids=lambda v: str(v))
+def test_run_time_k_shapes(tokens, experts, topk, hidden, inter, w4, gpu_device):
+    """Shapes the compile-time-K kernels do not take run on the matrix cores
+    (run-time-K MFMA kernels, or the W4 wave kernel) within tolerance of the
+    FP32 oracle (dequantised weights for W4)."""
+    x, gu, dn, ids, rw = O.make_inputs(tokens=tokens, experts=experts, topk=topk, hidden=hidden,
+                                       intermediate=inter, id_dtype=torch.int32, pattern="random",
+                                       seed=tokens + hidden + inter)
+    xd, dnd, idd, rwd = _to(gpu_device, x, dn, ids, rw)
+    if w4:
+        packed = quantize_gate_up(gu)
+        plan = prepare_w4_moe(xd, packed, dnd, idd, rwd)
+        ref_gu = O.dequantize_w4(packed.words, packed.scales)
+    else:
+        plan = prepare_moe(xd, gu.to(gpu_device), dnd, idd, rwd)
+        ref_gu = gu
+    assert plan.layout.fast_path == 0
+    out = plan.run().clone()
+    torch.cuda.synchronize()
+    assert plan.read_status() == 0
+    m = O.error(out, O.moe_reference(x, ref_gu, dn, ids, rw))
+    assert m["passed"], m
+
+
 def test_w4_m24_layout_entry(gpu_device):
     """prepare_w4_layout_moe on the reference's M24 physical layout
     (moe_weight_layout.py:81-127) is bitwise the v1 entry's result."""
