@@ -225,6 +225,40 @@ def test_run_time_k_shapes(tokens, experts, topk, hidden, inter, w4, gpu_device)
     assert m["passed"], m
 
 
+@pytest.mark.parametrize("tokens,experts,topk,hidden,inter,w4,block_m", [
+    (200, 1, 1, 96, 32, False, 16),    # one expert: 13 tasks of 16 rows, K = 1
+    (200, 1, 1, 96, 32, False, 64),    # 4 tasks of 64 rows, the last one ragged (8 rows)
+    (1, 3, 2, 160, 64, False, 32),     # T = 1: one row per task
+    (70, 2, 2, 128, 32, True, 64),     # W4: one 128-wide group per K-step
+    (33, 5, 3, 384, 96, True, 16),
+])
+def test_run_time_k_edges(tokens, experts, topk, hidden, inter, w4, block_m, gpu_device):
+    """Run-time-K kernels at their edges: minimal H and I, one expert with
+    many tasks, K = 1, T = 1, ragged last tasks, int64 IDs; bitwise equal
+    across two runs and within tolerance of the FP32 oracle."""
+    x, gu, dn, ids, rw = O.make_inputs(tokens=tokens, experts=experts, topk=topk, hidden=hidden,
+                                       intermediate=inter, id_dtype=torch.int64, pattern="random",
+                                       seed=7 * tokens + hidden)
+    xd, dnd, idd, rwd = _to(gpu_device, x, dn, ids, rw)
+    cfg = GemmConfig(block_m=block_m)
+    if w4:
+        packed = quantize_gate_up(gu)
+        plan = prepare_w4_moe(xd, packed, dnd, idd, rwd, down_config=cfg)
+        ref_gu = O.dequantize_w4(packed.words, packed.scales)
+    else:
+        plan = prepare_moe(xd, gu.to(gpu_device), dnd, idd, rwd, config=cfg)
+        ref_gu = gu
+    assert plan.layout.fast_path == 0 and plan.layout.token_block == block_m
+    a = plan.run().clone()
+    b = plan.run().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert plan.read_status() == 0
+    _check_dispatch(plan, ids, experts)
+    m = O.error(a, O.moe_reference(x, ref_gu, dn, ids, rw))
+    assert m["passed"], m
+
+
 def test_w4_m24_layout_entry(gpu_device):
     """prepare_w4_layout_moe on the reference's M24 physical layout
     (moe_weight_layout.py:81-127) is bitwise the v1 entry's result."""
