@@ -333,6 +333,7 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
 constexpr int kMultiThreads = 1024;
 constexpr int kMultiWaves = kMultiThreads / kWave;
 constexpr int kMultiSpinCap = 1 << 20;
+constexpr int kMultiBatch = 16;  // published words read per thread per round trip
 
 __device__ __forceinline__ uint32_t coherent_load(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -358,13 +359,15 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   const int tpw = a.plan_tpw;
   const int t0 = w * tpw, t1 = min(a.T, t0 + tpw);
   const int q0 = t0 * K, nq = (t1 - t0) * K;  // <= kMultiThreads
-  const uint32_t tag = epoch_tag(coherent_load(a.status + 2));
   uint32_t *const part = (uint32_t *)a.partials;
 
-  // 1. routes of this chunk into LDS.
+  // 1. routes of this chunk into LDS.  The logits are requested before the
+  // epoch word, whose device-coherent load is another memory round trip:
+  // the two overlap instead of the logits waiting behind it.
   float raw[4];
   const int rt = t0 + wave;
   if (ROUTER) load_token_logits<false>(a.logits, rt, rt < t1, E, raw);
+  const uint32_t epoch = coherent_load(a.status + 2);
   if (tid == 0) {
     s_flags = 0;
     s_all_flags = 0;
@@ -383,6 +386,7 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
     }
   }
   __syncthreads();
+  const uint32_t tag = epoch_tag(__builtin_amdgcn_readfirstlane(epoch));
 
   // 2. chunk-local canonical ranks and per-expert counts.
   const bool valid = tid < nq;
@@ -420,9 +424,10 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   if (ok) s_lrank[tid] = s_wcnt[wave][id] + lrank;
 
   // 4. every chunk's counts.  The W x (E + 1) published words are spread over
-  // the workgroup's threads, eight per request batch: all eight loads are in
-  // flight before any tag is checked (one memory round trip per batch, not
-  // per word), and only a word whose tag has not arrived is read again.
+  // the workgroup's threads, kMultiBatch per request batch: all of a batch's
+  // loads are in flight before any tag is checked (one memory round trip per
+  // batch, not per word; 64 router workgroups x 129 words at T = 1024 fit one
+  // batch of 16 per thread, where 8 per thread needed a second round trip).
   // Integer sums, so the order of the LDS additions does not matter.
   for (int e = tid; e < E; e += kMultiThreads) {
     s_base[e] = 0;
@@ -433,19 +438,19 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   {
     const int nwords = W * (E + 1);
     uint32_t fl = 0;
-    for (int j0 = 0; j0 < nwords; j0 += 8 * kMultiThreads) {
-      uint32_t v[8];
-      // The whole batch is re-read (all eight loads in flight again) until
+    for (int j0 = 0; j0 < nwords; j0 += kMultiBatch * kMultiThreads) {
+      uint32_t v[kMultiBatch];
+      // The whole batch is re-read (all its loads in flight again) until
       // every tag has arrived.
       for (int n = 0;; ++n) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kMultiBatch; ++i) {
           const int j = j0 + i * kMultiThreads + tid;
           v[i] = j < nwords ? coherent_load(part + j) : (tag << 16);
         }
         bool all = true;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) all &= (v[i] >> 16) == tag;
+        for (int i = 0; i < kMultiBatch; ++i) all &= (v[i] >> 16) == tag;
         if (all) break;
         if (n >= kMultiSpinCap) {
           stalled = true;
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
         __builtin_amdgcn_s_sleep(1);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kMultiBatch; ++i) {
         const int j = j0 + i * kMultiThreads + tid;
         if (j >= nwords) continue;
         const uint32_t c = v[i] & 0xffffu;
