@@ -363,10 +363,17 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
 
   // 1. routes of this chunk into LDS.  The logits are requested before the
   // epoch word, whose device-coherent load is another memory round trip:
-  // the two overlap instead of the logits waiting behind it.
+  // the two overlap instead of the logits waiting behind it.  With E <= 128
+  // each token is routed by a half-wave, so the chunk's 16 tokens take 8
+  // waves (2 per SIMD) instead of 16: the routing chains are bound by SIMD
+  // issue, and this halves it.
   float raw[4];
-  const int rt = t0 + wave;
-  if (ROUTER) load_token_logits<false>(a.logits, rt, rt < t1, E, raw);
+  const bool half = ROUTER && E <= 128;
+  const int rt = half ? t0 + 2 * wave + (lane >> 5) : t0 + wave;
+  if (ROUTER) {
+    if (half) load_token_logits<true>(a.logits, rt, rt < t1, E, raw);
+    else load_token_logits<false>(a.logits, rt, rt < t1, E, raw);
+  }
   const uint32_t epoch = coherent_load(a.status + 2);
   if (tid == 0) {
     s_flags = 0;
@@ -375,9 +382,14 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   for (int i = tid; i < kMultiWaves * kMaxExperts; i += kMultiThreads) (&s_wcnt[0][0])[i] = 0;
   uint32_t flags = 0;
   if constexpr (ROUTER) {
-    if (rt < t1)
+    if (half) {
+      if (t0 + 2 * wave < t1)  // wave-uniform: the wave's first token exists
+        route_token<true>(raw, rt, rt < t1, E, K, a.renormalize, (int32_t *)a.ids, a.weights,
+                          flags, s_ids - q0, s_w - q0);
+    } else if (rt < t1) {
       route_token<false>(raw, rt, true, E, K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
                          s_ids - q0, s_w - q0);
+    }
   } else {
     if (tid < nq) {
       const long long idv = (long long)((const IdT *)a.ids)[q0 + tid];
