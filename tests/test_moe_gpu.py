@@ -395,12 +395,13 @@ def test_non_default_stream(gpu_device):
 
 
 @pytest.mark.parametrize("tokens,experts,k", [(17, 128, 8), (32, 128, 8), (31, 60, 1), (20, 8, 2),
-                                              (25, 128, 32), (16, 100, 3), (18, 33, 5)])
+                                              (25, 128, 32), (16, 100, 3), (18, 33, 5),
+                                              (12, 256, 8), (16, 160, 16)])
 def test_fused_router_two_tokens_per_wave(tokens, experts, k, gpu_device):
     """The planner routes 17..32 tokens two per wave when E <= 128 (and one per
-    wave up to 16): IDs bit-exact with the oracle's top-k on logits full of ties
-    (ties go to the lower expert), weights to fp32 rounding, the layer within
-    tolerance, and a NaN logit raises status bit 2."""
+    wave up to 16, e.g. E = 160 or 256): IDs bit-exact with the oracle's top-k
+    on logits full of ties (ties go to the lower expert), weights to fp32
+    rounding, the layer within tolerance, and a NaN logit raises status bit 2."""
     x, gu, dn, _, _ = O.make_inputs(tokens=tokens, experts=experts, topk=k, hidden=128,
                                     intermediate=128, id_dtype=torch.int32, pattern="random",
                                     seed=tokens + experts)
