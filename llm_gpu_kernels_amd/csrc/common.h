@@ -65,30 +65,24 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 // W4G128 decode: packed word of eight int4 (nibble = q + 8, earliest K in the
 // low nibble) -> eight bf16 values bf16_rn(q * scale), packed in pairs.
 //
-// Nibble n sitting at bits 4p..4p+3 (p = 2, 3, 4: inside the 23-bit mantissa)
-// of a word whose other bits are replaced by those of 2^23 (one v_bfi_b32)
-// reads as the float 2^23 + n * 16^p.  With per-group constants
-// sp = s * 16^-p and cp = -(2^(23-4p) + 8) * s (both exact: power-of-two
-// scaling, and an 8-bit-significand scale times an integer of at most 13
-// significant bits),
-//   fma(2^23 + n * 16^p, sp, cp) = (2^(23-4p) + n) s - (2^(23-4p) + 8) s
-//                                = (n - 8) s  exactly (<= 12 significant bits),
-// so the only rounding is the final bf16 conversion -- the same as rounding
-// float(q) * float(scale).  Nibbles 2..4 decode in place, nibbles 0..1 from
-// w << 8 and nibbles 5..7 from w >> 12.
+// One bit insert places two nibbles, one per 16-bit half, into the mantissa
+// of the fp16 number 1024 (0x6400, ulp 1): at bits 0..3 a half reads as
+// 1024 + n, at bits 4..7 as 1024 + 16 n.  gfx950's v_fma_mix_f32 takes either
+// half as an fp16 operand of a single-rounding fp32 FMA, so with per-group
+// constants (all exact: power-of-two scaling, and an 8-bit-significand scale
+// times 1032 = 2^10 + 2^3 or 72 = 2^6 + 2^3)
+//   fma(1024 + n,    s,      -1032 s) = (n - 8) s
+//   fma(1024 + 16 n, s / 16, -72 s)   = (n - 8) s
+// exactly (<= 12 significant bits), and the only rounding is the final bf16
+// conversion -- the same as rounding float(q) * float(scale).  Per eight
+// weights: one shift, four bit inserts, eight FMAs, four bf16 packs.  (q = 0
+// decodes as +0 whatever the scale's sign; the quantizer's scales are >= 0.)
 struct W4Scale {
-  float sp[3], cp[3];  // p = 2, 3, 4
+  float s, c0, s16, c1;
 };
 
 __device__ __forceinline__ W4Scale w4_scale(float s) {
-  W4Scale k;
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int p = i + 2;
-    k.sp[i] = s * __uint_as_float((uint32_t)(127 - 4 * p) << 23);  // s * 2^-4p
-    k.cp[i] = -s * (float)((1 << (23 - 4 * p)) + 8);
-  }
-  return k;
+  return W4Scale{s, -1032.0f * s, s * 0.0625f, -72.0f * s};
 }
 
 // (mask & src) | (~mask & other), as gfx950's three-input bit operation
@@ -100,18 +94,26 @@ __device__ __forceinline__ uint32_t bfi_b32(uint32_t mask, uint32_t src, uint32_
   return d;
 }
 
+// fma(float(fp16 half HI of h2), s, c): one v_fma_mix_f32 (the compiler
+// folds the half select and the fp16 -> fp32 conversion into the FMA).
+template <int HI>
+__device__ __forceinline__ float fma_mix(uint32_t h2, float s, float c) {
+  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(HI ? h2 >> 16 : h2 & 0xffffu));
+  return __builtin_fmaf((float)h, s, c);
+}
+
 __device__ __forceinline__ u32x4 w4_decode8(uint32_t w, const W4Scale &k) {
-  const uint32_t magic = 0x4b000000u;  // 2^23: exponent bits only, empty mantissa
-  const uint32_t lo = w << 8, hi = w >> 12;
-  auto dq = [&](uint32_t src, int p) {
-    return __builtin_fmaf(__uint_as_float(bfi_b32(0xfu << (4 * p), src, magic)), k.sp[p - 2],
-                          k.cp[p - 2]);
-  };
+  const uint32_t magic = 0x64006400u;  // fp16 1024 in both halves
+  const uint32_t w8 = w >> 8;
+  const uint32_t a = bfi_b32(0x000f000fu, w, magic);   // 1024 + n0      | 1024 + n4
+  const uint32_t b = bfi_b32(0x00f000f0u, w, magic);   // 1024 + 16 n1   | 1024 + 16 n5
+  const uint32_t c = bfi_b32(0x000f000fu, w8, magic);  // n2 | n6
+  const uint32_t d = bfi_b32(0x00f000f0u, w8, magic);  // n3 | n7
   u32x4 r;
-  r[0] = pack_bf16x2(dq(lo, 2), dq(lo, 3));  // nibbles 0, 1
-  r[1] = pack_bf16x2(dq(w, 2), dq(w, 3));    // nibbles 2, 3
-  r[2] = pack_bf16x2(dq(w, 4), dq(hi, 2));   // nibbles 4, 5
-  r[3] = pack_bf16x2(dq(hi, 3), dq(hi, 4));  // nibbles 6, 7
+  r[0] = pack_bf16x2(fma_mix<0>(a, k.s, k.c0), fma_mix<0>(b, k.s16, k.c1));
+  r[1] = pack_bf16x2(fma_mix<0>(c, k.s, k.c0), fma_mix<0>(d, k.s16, k.c1));
+  r[2] = pack_bf16x2(fma_mix<1>(a, k.s, k.c0), fma_mix<1>(b, k.s16, k.c1));
+  r[3] = pack_bf16x2(fma_mix<1>(c, k.s, k.c0), fma_mix<1>(d, k.s16, k.c1));
   return r;
 }
 
