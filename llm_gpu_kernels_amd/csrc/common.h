@@ -62,27 +62,39 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// Loads from a wave-uniform base plus a 32-bit per-lane byte offset, as
+// buffer loads: the base goes into a scalar resource and no lane computes a
+// 64-bit address.  `base` must be the same in every lane of the wave.
+__device__ __forceinline__ u32x4 load_u128_at(const void *base, uint32_t off) {
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t load_u16_at(const void *base, uint32_t off) {
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+}
+
 // W4G128 decode: packed word of eight int4 (nibble = q + 8, earliest K in the
 // low nibble) -> eight bf16 values bf16_rn(q * scale), packed in pairs.
 //
 // One bit insert places two nibbles, one per 16-bit half, into the mantissa
-// of the fp16 number 1024 (0x6400, ulp 1): at bits 0..3 a half reads as
-// 1024 + n, at bits 4..7 as 1024 + 16 n.  gfx950's v_fma_mix_f32 takes either
-// half as an fp16 operand of a single-rounding fp32 FMA, so with per-group
-// constants (all exact: power-of-two scaling, and an 8-bit-significand scale
-// times 1032 = 2^10 + 2^3 or 72 = 2^6 + 2^3)
-//   fma(1024 + n,    s,      -1032 s) = (n - 8) s
-//   fma(1024 + 16 n, s / 16, -72 s)   = (n - 8) s
+// of an fp16 number: nibbles at bits 0..3 of a half under the exponent of
+// 1024 (0x6400, ulp 1) read as 1024 + n, nibbles at bits 4..7 under the
+// exponent of 64 (0x5400, ulp 1/16) as 64 + n.  gfx950's v_fma_mix_f32 takes
+// either half as an fp16 operand of a single-rounding fp32 FMA, so with
+// per-group constants (exact: an 8-bit-significand scale times
+// 1032 = 2^10 + 2^3 or 72 = 2^6 + 2^3)
+//   fma(1024 + n, s, -1032 s) = fma(64 + n, s, -72 s) = (n - 8) s
 // exactly (<= 12 significant bits), and the only rounding is the final bf16
 // conversion -- the same as rounding float(q) * float(scale).  Per eight
 // weights: one shift, four bit inserts, eight FMAs, four bf16 packs.  (q = 0
 // decodes as +0 whatever the scale's sign; the quantizer's scales are >= 0.)
 struct W4Scale {
-  float s, c0, s16, c1;
+  float s, c0, c1;
 };
 
 __device__ __forceinline__ W4Scale w4_scale(float s) {
-  return W4Scale{s, -1032.0f * s, s * 0.0625f, -72.0f * s};
+  return W4Scale{s, -1032.0f * s, -72.0f * s};
 }
 
 // (mask & src) | (~mask & other), as gfx950's three-input bit operation
@@ -103,17 +115,17 @@ __device__ __forceinline__ float fma_mix(uint32_t h2, float s, float c) {
 }
 
 __device__ __forceinline__ u32x4 w4_decode8(uint32_t w, const W4Scale &k) {
-  const uint32_t magic = 0x64006400u;  // fp16 1024 in both halves
+  const uint32_t m0 = 0x64006400u, m1 = 0x54005400u;  // fp16 1024 / 64 in both halves
   const uint32_t w8 = w >> 8;
-  const uint32_t a = bfi_b32(0x000f000fu, w, magic);   // 1024 + n0      | 1024 + n4
-  const uint32_t b = bfi_b32(0x00f000f0u, w, magic);   // 1024 + 16 n1   | 1024 + 16 n5
-  const uint32_t c = bfi_b32(0x000f000fu, w8, magic);  // n2 | n6
-  const uint32_t d = bfi_b32(0x00f000f0u, w8, magic);  // n3 | n7
+  const uint32_t a = bfi_b32(0x000f000fu, w, m0);   // 1024 + n0 | 1024 + n4
+  const uint32_t b = bfi_b32(0x00f000f0u, w, m1);   //   64 + n1 |   64 + n5
+  const uint32_t c = bfi_b32(0x000f000fu, w8, m0);  // n2 | n6
+  const uint32_t d = bfi_b32(0x00f000f0u, w8, m1);  // n3 | n7
   u32x4 r;
-  r[0] = pack_bf16x2(fma_mix<0>(a, k.s, k.c0), fma_mix<0>(b, k.s16, k.c1));
-  r[1] = pack_bf16x2(fma_mix<0>(c, k.s, k.c0), fma_mix<0>(d, k.s16, k.c1));
-  r[2] = pack_bf16x2(fma_mix<1>(a, k.s, k.c0), fma_mix<1>(b, k.s16, k.c1));
-  r[3] = pack_bf16x2(fma_mix<1>(c, k.s, k.c0), fma_mix<1>(d, k.s16, k.c1));
+  r[0] = pack_bf16x2(fma_mix<0>(a, k.s, k.c0), fma_mix<0>(b, k.s, k.c1));
+  r[1] = pack_bf16x2(fma_mix<0>(c, k.s, k.c0), fma_mix<0>(d, k.s, k.c1));
+  r[2] = pack_bf16x2(fma_mix<1>(a, k.s, k.c0), fma_mix<1>(b, k.s, k.c1));
+  r[3] = pack_bf16x2(fma_mix<1>(c, k.s, k.c0), fma_mix<1>(d, k.s, k.c1));
   return r;
 }
 

@@ -87,8 +87,8 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
     for (int rb = 0; rb < NRB; ++rb) {
       if constexpr (W4) {
         const size_t u = w4unit[rb] + st;
-        ra[d][rb] = ((const u32x4 *)a.w4_words)[u * kWave + lane];
-        rs[d][rb] = a.w4_scales[u * 16 + r];
+        ra[d][rb] = load_u128_at((const uint8_t *)a.w4_words + u * (kWave * 16), (uint32_t)lane * 16u);
+        rs[d][rb] = load_u16_at((const uint8_t *)a.w4_scales + u * 32, (uint32_t)r * 2u);
       } else {
         ra[d][rb] = *(const u32x4 *)(arow[rb] + st * 32);
       }

@@ -95,8 +95,8 @@ __global__ __launch_bounds__(kThreads, 4) void wave_w4_kernel(ExpertArgs a) {
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       const size_t u = rbi[rb] + s;
-      slot[rb] = ((const u32x4 *)a.w4_words)[u * kWave + lane];
-      sslot[rb] = a.w4_scales[u * 16 + r];
+      slot[rb] = load_u128_at((const uint8_t *)a.w4_words + u * (kWave * 16), (uint32_t)lane * 16u);
+      sslot[rb] = load_u16_at((const uint8_t *)a.w4_scales + u * 32, (uint32_t)r * 2u);
     }
   };
   if (active) {
