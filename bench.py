@@ -36,6 +36,13 @@ WORKLOADS = {
     "qwen-w4-t193": dict(shape="qwen", T=193, routing="uniform", w4=True),
     "qwen-w4-t1024": dict(shape="qwen", T=1024, routing="uniform", w4=True),
     "tiny-bf16-t17": dict(shape="tiny", T=17, routing="uniform", w4=False),
+    # One GPU's share of the Qwen layer under 8-way expert / tensor parallelism
+    # (the local kernels at their real shard shapes; no collectives).
+    "qwen-ep8-bf16-t17": dict(shape="qwen-ep8", T=17, routing="uniform", w4=False),
+    "qwen-ep8-bf16-t1024": dict(shape="qwen-ep8", T=1024, routing="uniform", w4=False),
+    "qwen-tp8-bf16-t17": dict(shape="qwen-tp8", T=17, routing="uniform", w4=False),
+    "qwen-tp8-bf16-t1024-zipf": dict(shape="qwen-tp8", T=1024, routing="zipf", w4=False),
+    "qwen-tp8-w4-t17": dict(shape="qwen-tp8", T=17, routing="uniform", w4=True),
 }
 
 

@@ -17,6 +17,15 @@
 //    straight from global memory into a register ring kFlexRing steps ahead;
 //  * the eight partial tiles are summed through LDS in fixed wave order and
 //    the epilogue applies the reference's rounding stages.
+//
+// With few K-steps (e.g. the down projection of one GPU's share I = 96 under
+// tensor parallelism) splitting K would leave waves idle and cost a cross-wave
+// sum per unit, so the waves split the columns instead: a unit is (task, eight
+// column blocks), wave w takes column block 8 g + w over the whole K and
+// stores its own outputs (no LDS, no barrier).  Which split is faster depends
+// on K and on the rows per task (measured over H, I in 320 .. 2880 with 16-
+// and 64-row tasks): columns up to K = 384 / 768 / 1536 for 16 / 32 / 64-row
+// tasks, K beyond.
 #include "common.h"
 #include "moe_internal.h"
 
@@ -32,7 +41,11 @@ constexpr int kWaves = kThreads / kWave;
 template <bool W4>
 constexpr int kFlexRing = W4 ? 2 : 4;
 
-template <int KIND, int MT, bool W4>
+// K at or below which the waves split the columns instead of K, by token
+// blocks per task.
+constexpr int column_k(int MT) { return MT == 1 ? 384 : MT == 2 ? 768 : 1536; }
+
+template <int KIND, int MT, bool W4, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
   static_assert(!W4 || KIND == 0, "W4G128 holds the gate/up weights only");
   constexpr int NRB = 2;
@@ -42,18 +55,24 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
 
   const int H = a.H, I = a.I;
   const int ncb = KIND == 0 ? I / 16 : H / 32;
-  const int task = blockIdx.x / ncb, cb = blockIdx.x - (blockIdx.x / ncb) * ncb;
-  if (task >= *a.num_tasks) return;
-  const int4 tk = a.tasks[task];
-  const int expert = tk.x, row0 = tk.y, rows = tk.z;
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & (kWave - 1);
   const int r = lane & 15, g = lane >> 4;
+  // Unit of this workgroup: (task, column block) or, without the K split,
+  // (task, group of kWaves column blocks).
+  const int per_task = SPLIT ? ncb : (ncb + kWaves - 1) / kWaves;
+  const int task = blockIdx.x / per_task, ub = blockIdx.x - task * per_task;
+  const int cb = SPLIT ? ub : ub * kWaves + wave;
+  if (task >= *a.num_tasks || cb >= ncb) return;  // no barrier follows without the split
+  const int4 tk = a.tasks[task];
+  const int expert = tk.x, row0 = tk.y, rows = tk.z;
+
   const int K = KIND == 0 ? H : I;
   const int nsteps = W4 ? K / 128 : K / 32;
-  const int mine = wave < nsteps ? (nsteps - 1 - wave) / kWaves + 1 : 0;
+  // K-steps of this wave: w, w + 8, ... with the split, all of them without.
+  const int mine = SPLIT ? (wave < nsteps ? (nsteps - 1 - wave) / kWaves + 1 : 0) : nsteps;
+  const int sfirst = SPLIT ? wave : 0, sstride = SPLIT ? kWaves : 1;
 
   // Token rows of this lane's B fragments (rows past the task's end read the
   // task's first row: finite data in columns the epilogue never stores).
@@ -82,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
   u32x4 ra[D][NRB], rbuf[D][MT][KPS];
   uint32_t rs[D][NRB];
   auto load = [&](int j, int d) __attribute__((always_inline)) {
-    const int st = wave + j * kWaves;
+    const int st = sfirst + j * sstride;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       if constexpr (W4) {
@@ -137,6 +156,40 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
     }
   }
 
+  if constexpr (!SPLIT) {
+    // Output (rb, mt, i) of this lane: weight row 16 rb + 4 g + i of the
+    // block, token row mt * 16 + r of the task; four consecutive columns,
+    // one 8-byte store.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int j = mt * 16 + r;
+      if (j >= rows) continue;
+      if constexpr (KIND == 0) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gt = bf16_round(acc[0][mt][i]);
+          const float up = bf16_round(acc[1][mt][i]);
+          v[i] = gt / (1.0f + expf(-gt)) * up;
+        }
+        u32x2 packed;
+        packed[0] = pack_bf16x2(v[0], v[1]);
+        packed[1] = pack_bf16x2(v[2], v[3]);
+        *(u32x2 *)(a.act + (size_t)(row0 + j) * I + cb * 16 + 4 * g) = packed;
+      } else {
+        const size_t q = (size_t)a.row_route[row0 + j];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+          u32x2 packed;
+          packed[0] = pack_bf16x2(acc[rb][mt][0], acc[rb][mt][1]);
+          packed[1] = pack_bf16x2(acc[rb][mt][2], acc[rb][mt][3]);
+          *(u32x2 *)(a.routed + q * H + cb * 32 + rb * 16 + 4 * g) = packed;
+        }
+      }
+    }
+    return;
+  }
+
   // Fixed-order sum of the eight K-slices.
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb)
@@ -178,10 +231,16 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
 template <int KIND, int MT, bool W4>
 hipError_t launch_mt(const ExpertArgs &a, int task_capacity, hipStream_t s) {
   const int ncb = KIND == 0 ? a.I / 16 : a.H / 32;
+  if ((KIND == 0 ? a.H : a.I) <= column_k(MT)) {
+    const long long grid = (long long)task_capacity * ((ncb + kWaves - 1) / kWaves);
+    if (grid <= 0) return hipSuccess;
+    hipLaunchKernelGGL((flex_kernel<KIND, MT, W4, false>), dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+  }
   const long long grid = (long long)task_capacity * ncb;
   if (grid <= 0) return hipSuccess;
   const size_t lds = (size_t)kWaves * 2 * MT * kWave * sizeof(f32x4);
-  auto k = flex_kernel<KIND, MT, W4>;
+  auto k = flex_kernel<KIND, MT, W4, true>;
   static const bool attr = hipFuncSetAttribute((const void *)k,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds) == hipSuccess;

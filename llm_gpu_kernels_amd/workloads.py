@@ -2,6 +2,12 @@
 
 * ``tiny``: T tokens, H=512, I=256, E=8, top-2 (CPU-reference sized).
 * ``qwen``: Qwen3-30B-A3B MoE shape, H=2048, I=768, E=128, top-8.
+* ``qwen-ep8``: one GPU's share of that layer under 8-way expert parallelism:
+  its 16 experts, and one route per received row (the dispatch all-to-all
+  delivers each (token, local expert) pair as a row; T rows here).
+* ``qwen-tp8``: one GPU's share under 8-way tensor parallelism: all 128
+  experts with I = 768 / 8 = 96 (gate/up rows and down columns sharded); the
+  partial [T, H] outputs would then be summed across GPUs.
 Weights ~ N(0, 0.02) bf16, hidden ~ N(0, 1) bf16, router logits ~ N(0, 1)
 fp32.  ``routing="zipf"`` adds log(Zipf(s=1.2)) over a seeded expert
 permutation to the logits, so a few experts receive hundreds of rows and many
@@ -15,6 +21,8 @@ import torch
 SHAPES = {
     "tiny": dict(E=8, H=512, I=256, K=2),
     "qwen": dict(E=128, H=2048, I=768, K=8),
+    "qwen-ep8": dict(E=16, H=2048, I=768, K=1),
+    "qwen-tp8": dict(E=128, H=2048, I=96, K=8),
 }
 
 

@@ -115,7 +115,7 @@ CONFIGS = [("tiny", 17, "uniform"), ("qwen", 17, "uniform"), ("qwen", 193, "unif
            ("qwen", 1024, "zipf"), ("qwen", 1024, "uniform")]
 
 
-def _routed_parity(shape, tokens, routing, gpu_device, w4=False):
+def _routed_parity(shape, tokens, routing, gpu_device, w4=False, expect_path=None):
     lay = make_layer(shape, tokens, routing=routing, seed=0, device=gpu_device)
     k = lay["K"]
     gate_up = lay["gate_up"]
@@ -131,7 +131,8 @@ def _routed_parity(shape, tokens, routing, gpu_device, w4=False):
     else:
         weights_for_oracle = gate_up.cpu()
     plan = prepare_routed_moe(lay["x"], lay["logits"], gate_up, lay["down"], k)
-    expect_path = 2 if tokens * k >= 32 * lay["E"] else 1
+    if expect_path is None:
+        expect_path = 2 if tokens * k >= 32 * lay["E"] else 1
     assert plan.layout.fast_path == expect_path
     out = plan.forward(lay["x"], lay["logits"])
     torch.cuda.synchronize()
@@ -155,6 +156,19 @@ def test_routed_bf16_layer(shape, tokens, routing, gpu_device):
 @pytest.mark.parametrize("tokens", [17, 193, 1024])
 def test_routed_w4_layer(tokens, gpu_device):
     _routed_parity("qwen", tokens, "uniform", gpu_device, w4=True)
+
+
+# One GPU's share of the Qwen layer under 8-way expert parallelism (16 experts,
+# one route per row: the streaming and the tiled kernels) and tensor parallelism
+# (I = 96: the run-time-K kernels), as the bench measures them.
+SHARD_CONFIGS = [("qwen-ep8", 17, "uniform", False, 1), ("qwen-ep8", 1024, "uniform", False, 2),
+                 ("qwen-tp8", 17, "uniform", False, 0), ("qwen-tp8", 1024, "zipf", False, 0),
+                 ("qwen-tp8", 17, "uniform", True, 0)]
+
+
+@pytest.mark.parametrize("shape,tokens,routing,w4,path", SHARD_CONFIGS, ids=lambda v: str(v))
+def test_parallel_shard_shapes(shape, tokens, routing, w4, path, gpu_device):
+    _routed_parity(shape, tokens, routing, gpu_device, w4=w4, expect_path=path)
 
 
 @pytest.mark.parametrize("tokens", [17, 193])
@@ -197,6 +211,11 @@ FLEX_SHAPES = [
     (9, 8, 2, 1152, 384, True),      # W4 run-time-K gate/up, 16-row tasks
     (100, 8, 2, 1152, 384, True),    # 32-row tasks
     (300, 8, 2, 1152, 384, True),    # 64-row tasks
+    # K <= 256: the waves split the columns instead of K (gate/up at H = 256,
+    # down at I = 96: one GPU's share of the Qwen layer under 8-way tensor parallelism)
+    (100, 8, 2, 256, 96, False),     # 32-row tasks, both GEMMs column-split
+    (300, 8, 2, 2048, 96, False),    # 64-row tasks, gate/up K-split, down column-split
+    (17, 8, 4, 256, 96, True),       # W4 gate/up with two 128-wide groups, column-split
 ]
 
 
