@@ -1,6 +1,6 @@
 """Benchmark of the MI355X MoE forward (one GPU).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload qwen-bf16-t17]
+    python bench.py [--gpus 1] [--steps 64] [--warmup 10] [--workload qwen-bf16-t17]
 
 A step is one full router-inclusive MoE layer forward (router -> planner ->
 gate/up+SwiGLU -> down -> combine) over inputs already resident in HBM,
@@ -332,7 +332,7 @@ def _attach_cpu(rec, cpu):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="qwen-bf16-t17", choices=sorted(WORKLOADS))
     ap.add_argument("--no-sweep", action="store_true")
