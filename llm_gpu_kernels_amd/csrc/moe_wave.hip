@@ -140,6 +140,8 @@ __global__ __launch_bounds__(kThreads, 4) void wave_w4_kernel(ExpertArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Token blocks holding rows of this task (wave-uniform).
+  const int nmt = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
   // Group s (ring slot d) against chunk buffer `buf`, whose first group is s0c.
   auto step = [&](int s, auto d_tag, int buf, int s0c) __attribute__((always_inline)) {
     constexpr int d = decltype(d_tag)::value;
@@ -155,6 +157,7 @@ __global__ __launch_bounds__(kThreads, 4) void wave_w4_kernel(ExpertArgs a) {
       const int c = 4 * (4 * (s - s0c) + j) + g;  // 16-byte chunk of k-step within the chunk
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
+        if (mt > 0 && mt >= nmt) break;  // 16-row blocks past the task's last row
         const u32x4 bf = *(const u32x4 *)(bb + b_off<KC>(mt * 16 + r, c));
         acc[0][mt] = mfma16(af0, bf, acc[0][mt]);
         acc[1][mt] = mfma16(af1, bf, acc[1][mt]);
