@@ -74,6 +74,9 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
   const int mine = SPLIT ? (wave < nsteps ? (nsteps - 1 - wave) / kWaves + 1 : 0) : nsteps;
   const int sfirst = SPLIT ? wave : 0, sstride = SPLIT ? kWaves : 1;
 
+  // Token blocks holding rows of this task (wave-uniform); the loads and
+  // MFMAs of the others are skipped.
+  const int nmt = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
   // Token rows of this lane's B fragments (rows past the task's end read the
   // task's first row: finite data in columns the epilogue never stores).
   const uint16_t *brow[MT];
@@ -113,10 +116,12 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt > 0 && mt >= nmt) break;  // token blocks past the task's last row
 #pragma unroll
       for (int ks = 0; ks < KPS; ++ks)
         rbuf[d][mt][ks] = *(const u32x4 *)(brow[mt] + (size_t)(st * KPS + ks) * 32);
+    }
   };
 
   f32x4 acc[NRB][MT];
@@ -133,11 +138,17 @@ __global__ __launch_bounds__(kThreads) void flex_kernel(ExpertArgs a) {
         for (int q = 0; q < 4; ++q) {
           const u32x4 af = w4_decode8(ra[d][rb][q], ks);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(af, rbuf[d][mt][q], acc[rb][mt]);
+          for (int mt = 0; mt < MT; ++mt) {
+            if (mt > 0 && mt >= nmt) break;
+            acc[rb][mt] = mfma16(af, rbuf[d][mt][q], acc[rb][mt]);
+          }
         }
       } else {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(ra[d][rb], rbuf[d][mt][0], acc[rb][mt]);
+        for (int mt = 0; mt < MT; ++mt) {
+          if (mt > 0 && mt >= nmt) break;
+          acc[rb][mt] = mfma16(ra[d][rb], rbuf[d][mt][0], acc[rb][mt]);
+        }
       }
     }
   };
