@@ -111,6 +111,40 @@ def test_tiled_path_forced(tokens, w4, gpu_device):
     assert m["passed"], m
 
 
+def _ids_with_counts(counts, tokens, k):
+    """[tokens, k] expert IDs whose per-expert counts are `counts` (each <= tokens):
+    route q = k_slot * tokens + t takes the q-th entry of the expert-sorted list, so
+    an expert's routes are consecutive q and land on distinct tokens."""
+    flat = torch.repeat_interleave(torch.arange(len(counts)), torch.tensor(counts))
+    assert flat.numel() == tokens * k and max(counts) <= tokens
+    return flat.view(k, tokens).t().contiguous().to(torch.int32)
+
+
+def test_w4_pair_passes_at_task_boundaries(gpu_device):
+    """W4 gate/up with 64-row tasks (the pair kernel): experts with 1, 33, 64, 65, 96,
+    97, 129 and 160 rows cover a single short task, a full task, two tasks run as one
+    96-row pass, two tasks run separately and three tasks; every grouped row is
+    checked against the FP32 oracle on the dequantised weights."""
+    tokens, k, e = 160, 8, 128
+    special = [96, 97, 65, 64, 129, 160, 1, 33]
+    rest = tokens * k - sum(special)
+    counts = special + [rest // (e - 8) + (1 if i < rest % (e - 8) else 0) for i in range(e - 8)]
+    ids = _ids_with_counts(counts, tokens, k)
+    lay = make_layer("qwen", tokens, seed=6, device=gpu_device)
+    w = torch.softmax(torch.randn(tokens, k, generator=torch.Generator().manual_seed(6)), dim=-1)
+    packed = quantize_gate_up(lay["gate_up"].cpu())
+    tiled = tile_gate_up(packed).to(gpu_device)
+    ref_gu = O.dequantize_w4(packed.words, packed.scales)
+    plan = prepare_w4_moe(lay["x"], tiled, lay["down"], ids.to(gpu_device), w.to(gpu_device),
+                          down_config=GemmConfig(block_m=64))
+    assert plan.layout.fast_path == 2
+    out = plan.run()
+    torch.cuda.synchronize()
+    assert plan.base.counts.cpu().tolist() == counts
+    m = O.error(out, O.moe_reference(lay["x"].cpu(), ref_gu, lay["down"].cpu(), ids.long(), w))
+    assert m["passed"], m
+
+
 CONFIGS = [("tiny", 17, "uniform"), ("qwen", 17, "uniform"), ("qwen", 193, "uniform"),
            ("qwen", 1024, "zipf"), ("qwen", 1024, "uniform")]
 
