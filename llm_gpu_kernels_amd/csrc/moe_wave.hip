@@ -218,13 +218,15 @@ hipError_t launch_mt(const ExpertArgs &a, int task_capacity, hipStream_t s) {
 
 
 // ---------------------------------------------------------------------------
-// 64-row tasks (T = 1024 class): one 32x32x16 A fragment per wave holds 16
+// W4 gate/up with whole-K waves: one 32x32x16 A fragment per wave holds 16
 // gate rows (fragment rows 0-15) and the 16 up rows of the same features
 // (rows 16-31), so the MFMA output puts gate and up of a (feature, token) in
 // the same lane (output rows 8q + 4h + i: q = 0, 1 gate, q = 2, 3 up).
 //
-// Unit = (pass, 16 intermediate columns).  A pass is one planner task, or two
-// consecutive 64-row tasks of an expert with at most 32*MT rows together, so
+// Launched for 64-row tasks (MT = 3) and, with several rows per expert, for
+// 16-row tasks (MT = 1).  Unit = (pass, 16 intermediate columns).  A pass is
+// one planner task, or two consecutive tasks of an expert with at most 32*MT
+// rows together, so
 // each weight is decoded once for every row of such an expert.  Per 16-K step
 // a wave decodes one packed int4 word per lane (w4_decode8, bit-exact with
 // the reference dequantisation) and multiplies it against up to MT 32-token
@@ -245,7 +247,6 @@ hipError_t launch_mt(const ExpertArgs &a, int task_capacity, hipStream_t s) {
 // (at most 128 VGPRs), the configuration that measured fastest against 12-wave
 // workgroups at three per SIMD, 8-wave ones at four, 256-K chunks and a
 // three-group weight ring.
-constexpr int kPairTask = 64;     // rows of a planner task (token_block 64)
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
@@ -253,8 +254,10 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 
 // NW waves per workgroup, MINW waves per SIMD (VGPR budget 512 / MINW),
 // NS = H / 128 groups along K, MT 32-token fragments per pass.
-template <int NW, int MINW, int NS, int MT, int D4, int kPairKC>
+// TB: rows of a planner task (token_block).
+template <int NW, int MINW, int NS, int MT, int D4, int kPairKC, int TB>
 __global__ __launch_bounds__(NW * 64, MINW) void pair_w4_kernel(ExpertArgs a) {
+  constexpr int kPairTask = TB;
   constexpr int kPairRowB = kPairKC * 2 + 16;  // padded LDS row
   constexpr int GPC = kPairKC / 128;           // int4 groups per chunk
   constexpr int ROWS = 32 * MT;                  // token rows per pass
@@ -310,8 +313,8 @@ __global__ __launch_bounds__(NW * 64, MINW) void pair_w4_kernel(ExpertArgs a) {
   for (int d = 0; d < D4; ++d) load_group(d, ring[d], sring[d]);
 
   // ---- token rows (B operand) -------------------------------------------------
-  // Piece i of a thread: row idx / 32, 16-byte chunk idx % 32 of the chunk's
-  // 256 K; rows past the pass's end load row 0 (finite data in columns the
+  // Piece i of a thread: row idx / (KC / 8), 16-byte chunk idx % (KC / 8) of
+  // the chunk; rows past the pass's end load row 0 (finite data in columns the
   // epilogue never stores).
   uint32_t bsrc[BPT], bdst[BPT];
 #pragma unroll
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(NW * 64, MINW) void pair_w4_kernel(ExpertArgs a) {
 // The 64-row-task kernel: H = 2048 (its unrolled group loop), I a multiple of
 // 16, and x small enough for 32-bit buffer offsets.
 bool pair_w4_ok(const ExpertArgs &a, int token_block) {
-  return token_block == kPairTask && a.H == 2048 && a.I % 16 == 0 &&
+  return (token_block == 64 || token_block == 16) && a.H == 2048 && a.I % 16 == 0 &&
          (long long)a.T * a.H * 2 < (1LL << 31);
 }
 
@@ -439,7 +442,10 @@ hipError_t launch_wave_w4_gate_up(const ExpertArgs &a, int task_capacity, int to
     const int groups = (a.I / 16 + NW - 1) / NW;
     const long long grid = (long long)task_capacity * groups;
     if (grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL((pair_w4_kernel<NW, 4, 16, 3, 2, 128>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+    if (token_block == 64)
+      hipLaunchKernelGGL((pair_w4_kernel<NW, 4, 16, 3, 2, 128, 64>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL((pair_w4_kernel<NW, 4, 16, 1, 2, 256, 16>), dim3((unsigned)grid), dim3(NW * 64), 0, s, a);
     return hipGetLastError();
   }
   switch (token_block) {
