@@ -35,6 +35,9 @@ WORKLOADS = {
     "qwen-w4-t17": dict(shape="qwen", T=17, routing="uniform", w4=True),
     "qwen-w4-t193": dict(shape="qwen", T=193, routing="uniform", w4=True),
     "qwen-w4-t1024": dict(shape="qwen", T=1024, routing="uniform", w4=True),
+    # The opt-in folded W4 decode (group scale on the fp32 group sum; effective
+    # weights q * scale, not the reference's bf16_rn(q * scale)).
+    "qwen-w4fold-t17": dict(shape="qwen", T=17, routing="uniform", w4=True, fold=True),
     "tiny-bf16-t17": dict(shape="tiny", T=17, routing="uniform", w4=False),
     # One GPU's share of the Qwen layer under 8-way expert / tensor parallelism
     # (the local kernels at their real shard shapes; no collectives).
@@ -67,7 +70,8 @@ def build_plans(spec, device, copies=2):
             dn = lay["down"].clone()
         else:
             gu, dn = gate_up.clone(), lay["down"].clone()
-        plans.append(prepare_routed_moe(lay["x"], lay["logits"], gu, dn, lay["K"]))
+        plans.append(prepare_routed_moe(lay["x"], lay["logits"], gu, dn, lay["K"],
+                                        w4_decode="fold" if spec.get("fold") else "exact"))
     torch.cuda.synchronize()
     return lay, plans
 
@@ -191,7 +195,8 @@ def measure(name, steps, warmup, device):
     tflops = alg["flops"] / (ms * 1e-3) / 1e12
     attainable = min(BF16_PEAK_TFLOPS, alg["flops"] / alg["layer_bytes"] * HBM_PEAK_GBS / 1e3)
     res = dict(
-        workload=name, T=t, weights="w4g128+bf16-down" if spec["w4"] else "bf16",
+        workload=name, T=t,
+        weights=("w4g128-fold+bf16-down" if spec.get("fold") else "w4g128+bf16-down") if spec["w4"] else "bf16",
         routing=spec["routing"], us_per_layer=round(ms * 1e3, 2),
         p50_us=round(statistics.median(samples) * 1e3, 2),
         p95_us=round(sorted(samples)[int(0.95 * (len(samples) - 1))] * 1e3, 2),

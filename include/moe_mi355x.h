@@ -53,6 +53,15 @@ extern "C" {
 #define MOE_WEIGHTS_BF16 0        /* gate_up bf16 [E, 2I, H]                  */
 #define MOE_WEIGHTS_W4G128 1      /* gate_up int4 in the tiled layout below;  *
                                    * needs H % 128 == 0 and I % 32 == 0        */
+/* The same W4G128 weights, opt-in folded decode: where a kernel implements it
+ * (the split-K streaming gate/up of the about-one-row-per-expert regime), the
+ * MFMAs run on the exact values 136 + q and each 128-K group's fp32 sum is
+ * scaled after subtracting 136 x the group's token sums, i.e. the effective
+ * weights are q * scale exactly instead of bf16_rn(q * scale) (no counterpart
+ * in the reference, whose kernels dequantise to bf16; within the layer
+ * tolerance, 7 instead of 17 decode instructions per 8 weights).  Other
+ * kernels keep the bit-exact bf16 decode. */
+#define MOE_WEIGHTS_W4G128_FOLD 2
 
 /* moe_desc.id_dtype */
 #define MOE_IDS_INT32 0

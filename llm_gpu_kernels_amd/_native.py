@@ -11,7 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoe_mi355x.so"
 
 MOE_OK, MOE_EINVAL, MOE_EDEVICE, MOE_ESPACE = 0, -1, -2, -3
-WEIGHTS_BF16, WEIGHTS_W4G128 = 0, 1
+WEIGHTS_BF16, WEIGHTS_W4G128, WEIGHTS_W4G128_FOLD = 0, 1, 2
 IDS_INT32, IDS_INT64 = 0, 1
 ROUTE_FIXED, ROUTE_LOGITS = 0, 1
 STATUS_BAD_ID, STATUS_BAD_WEIGHT, STATUS_BAD_LOGIT, STATUS_DIRTY_COUNTERS, STATUS_STALLED = 1, 2, 4, 8, 16

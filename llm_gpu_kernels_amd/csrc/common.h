@@ -129,4 +129,36 @@ __device__ __forceinline__ u32x4 w4_decode8(uint32_t w, const W4Scale &k) {
   return r;
 }
 
+// W4 "folded" decode for MFMA operands: one AND-OR per register places the
+// nibbles of a word's two 16-bit halves (k and k + 4 of the eight K values)
+// under the bf16 exponent of 128, i.e. the exact values 128 + n = 136 + q.
+// Register j holds (k_j, k_{j+4}), so the B operand must carry its K values
+// in the same order (w4_fold_b); the group scale and the -136 offset are
+// applied to the fp32 sum of the group's MFMAs.  Seven VALU instructions per
+// eight weights.
+__device__ __forceinline__ u32x4 w4_fold8(uint32_t w) {
+  const uint32_t m = 0x000f000fu, e = 0x43004300u;
+  u32x4 r;
+  r[0] = (w & m) | e;
+  r[1] = ((w >> 4) & m) | e;
+  r[2] = ((w >> 8) & m) | e;
+  r[3] = ((w >> 12) & m) | e;
+  return r;
+}
+// Natural-order bf16 x (x0 x1 | x2 x3 | x4 x5 | x6 x7) -> (x0 x4 | x1 x5 | x2 x6 | x3 x7).
+__device__ __forceinline__ u32x4 w4_fold_b(u32x4 x) {
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(x[2], x[0], 0x05040100u);
+  r[1] = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);
+  r[2] = __builtin_amdgcn_perm(x[3], x[1], 0x05040100u);
+  r[3] = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);
+  return r;
+}
+__device__ __forceinline__ float bf16x8_sum(u32x4 x) {
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t += bf16_bits_to_f32(x[i] & 0xffffu) + bf16_bits_to_f32(x[i] >> 16);
+  return t;
+}
+
 }  // namespace moe

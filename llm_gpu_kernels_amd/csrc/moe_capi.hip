@@ -48,6 +48,8 @@ int fuse_router_mode(const moe_desc *d) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+bool is_w4(int fmt) { return fmt == MOE_WEIGHTS_W4G128 || fmt == MOE_WEIGHTS_W4G128_FOLD; }
+
 // Shape-only kernel policy (never route contents, so a captured graph stays
 // valid when IDs change): mean rows per expert R/E below 32 -> weight
 // streaming with 16- or 32-row tasks; otherwise LDS-tiled GEMMs with 64-row
@@ -62,7 +64,7 @@ int choose_token_block(const moe_desc *d) {
 }
 
 int choose_path(const moe_desc *d, int tb) {
-  const bool w4 = d->weight_format == MOE_WEIGHTS_W4G128;
+  const bool w4 = is_w4(d->weight_format);
   if (tb == 64) {
     if (moe::tile_shape_ok(d->H, d->I, w4)) return moe::kTile;
     return moe::stream_shape_ok(d->H, d->I, w4) ? moe::kStream : moe::kGeneric;
@@ -80,7 +82,7 @@ int validate(const moe_desc *d) {
   const long long wide = d->H > 2LL * d->I ? d->H : 2LL * d->I;
   if (r >= (1LL << 31) || r * wide >= (1LL << 31))
     return fail(MOE_EINVAL, "R=T*K and R*max(H,2I) must be < 2^31");
-  if (d->weight_format != MOE_WEIGHTS_BF16 && d->weight_format != MOE_WEIGHTS_W4G128)
+  if (d->weight_format != MOE_WEIGHTS_BF16 && !is_w4(d->weight_format))
     return fail(MOE_EINVAL, "unknown weight format %d", d->weight_format);
   if (d->id_dtype != MOE_IDS_INT32 && d->id_dtype != MOE_IDS_INT64)
     return fail(MOE_EINVAL, "unknown id dtype %d", d->id_dtype);
@@ -93,7 +95,7 @@ int validate(const moe_desc *d) {
   if (d->token_block != 0 && d->token_block != 16 && d->token_block != 32 &&
       d->token_block != 64)
     return fail(MOE_EINVAL, "token_block must be 0, 16, 32 or 64");
-  if (d->weight_format == MOE_WEIGHTS_W4G128) {
+  if (is_w4(d->weight_format)) {
     if (!moe::flex_shape_ok(d->H, d->I, true))
       return fail(MOE_EINVAL, "W4G128 needs H %% 128 == 0 and I %% 32 == 0");
   }
@@ -103,7 +105,7 @@ int validate(const moe_desc *d) {
 // Router-fused bf16 shapes whose gate/up streams through LDS with 16-row
 // tasks plan in the gate/up prologue instead of a planner launch.
 bool planned_gate_up(const moe_desc *d, int path, int tb) {
-  return path == moe::kStream && tb == 16 && d->weight_format != MOE_WEIGHTS_W4G128 &&
+  return path == moe::kStream && tb == 16 && !is_w4(d->weight_format) &&
          moe::dma_plan_ok(d->H, d->I, d->T, d->K, d->E, fuse_router_mode(d));
 }
 
@@ -201,7 +203,7 @@ int bind_plan(moe_plan *p, const moe_desc *d) {
       return fail(MOE_EINVAL, "router mode needs logits");
     if (d->weight_format == MOE_WEIGHTS_BF16 && !d->gate_up)
       return fail(MOE_EINVAL, "null gate_up");
-    if (d->weight_format == MOE_WEIGHTS_W4G128 && (!d->w4_words || !d->w4_scales))
+    if (is_w4(d->weight_format) && (!d->w4_words || !d->w4_scales))
       return fail(MOE_EINVAL, "null W4 words/scales");
     if (((uintptr_t)d->workspace & 255u) != 0)
       return fail(MOE_EINVAL, "workspace must be 256-byte aligned");
@@ -214,9 +216,9 @@ int bind_plan(moe_plan *p, const moe_desc *d) {
   // kernel (tuned or run-time-K) reads 16-byte fragments: with an unaligned
   // buffer a bf16 forward takes the scalar kernels.
   const bool aligned = aligned16(d->x) && aligned16(d->down) && aligned16(d->out) &&
-                       (d->weight_format == MOE_WEIGHTS_W4G128 ? aligned16(d->w4_words)
+                       (is_w4(d->weight_format) ? aligned16(d->w4_words)
                                                                : aligned16(d->gate_up));
-  if (!aligned && d->weight_format == MOE_WEIGHTS_W4G128)
+  if (!aligned && is_w4(d->weight_format))
     return fail(MOE_EINVAL, "W4G128 buffers must be 16-byte aligned");
   if (!aligned) path = moe::kScalar;
   p->d = *d;
@@ -358,8 +360,9 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   xa.E = d.E;
   xa.K = d.K;
   xa.R = ra.R;
+  xa.w4_fold = d.weight_format == MOE_WEIGHTS_W4G128_FOLD ? 1 : 0;
 
-  const bool w4 = d.weight_format == MOE_WEIGHTS_W4G128;
+  const bool w4 = is_w4(d.weight_format);
   const bool router = ra.route_logits && !ra.fuse_router;
   int rc = MOE_OK;
   for (int st = first; st < last && rc == MOE_OK; ++st) {

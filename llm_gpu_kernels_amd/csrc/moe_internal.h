@@ -43,6 +43,7 @@ struct ExpertArgs {
   uint16_t *routed;            // [R, H] bf16, route order
   uint16_t *out;               // [T, H] bf16
   int T, H, I, E, K, R;
+  int w4_fold;                 // W4: folded decode where the kernel implements it (MOE_WEIGHTS_W4G128_FOLD)
 };
 
 // Router kernel for large T (one wave per token); folds its flags into status[1].

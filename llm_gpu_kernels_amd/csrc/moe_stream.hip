@@ -44,6 +44,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kWaitVmcntZero = (7 << 4) | (15 << 8);  // s_waitcnt vmcnt(0) only (gfx9 encoding)
 
+
 template <typename T>
 __device__ __forceinline__ const MOE_CONST T *as_const(const T *p) {
   return (const MOE_CONST T *)p;
@@ -60,8 +61,12 @@ __device__ __forceinline__ void lds_barrier() {
 // KIND 0: gate/up + SwiGLU.  A = gate rows cb*16.. and up rows I+cb*16..,
 //         K = H, B = x rows of the task's tokens.
 // KIND 1: down.  A = rows cb*32 + 16*rb (rb < 2), K = I, B = act rows.
-template <int KIND, int MT, int SPW, bool W4>
-__global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
+// FOLD (W4 only): the folded decode (w4_fold8): token fragments as the MFMA
+// A operand in the folded K order, weights (136 + q) as B, and each group's
+// fp32 sum scaled by the lane's own weight-row scale after subtracting 136 x
+// the group's token sums; effective weights q * scale exactly.
+template <int KIND, int MT, int SPW, bool W4, bool FOLD>
+__global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertArgs a) {
   constexpr int NRB = 2;
   extern __shared__ f32x4 s_red[];  // [2][kWaves][NRB][MT][64]
 
@@ -112,6 +117,33 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   // data that is never zeroed: an MFMA output column depends only on its own
   // B column and the epilogue never stores those columns.
   u32x4 bfr[MT][SPW];
+  // FOLD: the MFMA operands are swapped (token fragments A, weights B), so
+  // the output lane holds its own weight row (one scale per lane) and tokens
+  // 4g .. 4g + 3; xs holds -136 x (each group's sum of the 128 x values of
+  // those tokens), computed once per task.
+  static_assert(W4 || !FOLD, "the folded decode is a W4 mode");
+  constexpr int AWX = W4 ? SPW / 4 : 1;
+  // -136 x group sums per wave, [group][token], read back as f32x4 per group
+  // (in LDS rather than registers: the kernel is at its 128-VGPR budget).
+  float *s_xs = (float *)(s_red + 2 * kWaves * 2 * MT * kWave);  // after the partials
+  auto prep_b = [&]() {
+    if constexpr (FOLD) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < AWX; ++q) {
+          float t = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            t += bf16x8_sum(bfr[mt][4 * q + j]);
+            bfr[mt][4 * q + j] = w4_fold_b(bfr[mt][4 * q + j]);
+          }
+          t += __shfl_xor(t, 16, kWave);
+          t += __shfl_xor(t, 32, kWave);  // token r's group sum, in every lane of column r
+          if (g == 0) s_xs[(wave * AWX + q) * MT * 16 + mt * 16 + r] = -136.0f * t;
+        }
+    }
+  };
   auto load_b = [&](const Meta &m) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -135,16 +167,17 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   // of an unrolled loop: copying a register whose load is still in flight
   // would make the wave wait for it.
   constexpr int AW = W4 ? SPW / 4 : SPW;
-  constexpr int S = W4 ? 3 : 2;
+  constexpr int S = W4 && !FOLD ? 3 : 2;
   u32x4 aq[S][NRB][AW];
-  uint32_t sq[S][NRB][AW];
+  using ScaleT = uint32_t;  // the scale of the lane's own weight row
+  ScaleT sq[S][NRB][AW];
   Meta mq[S];
   // m.unit < 0 marks a ring slot past the end: it reads the first unit of the
   // weights (expert 0, column block 0), which every such slot shares through
   // the cache, with the normal lane offsets -- so every address is a scalar
   // base plus a fixed per-lane offset and the loads need no vector math.
   const uint32_t lane_a = KIND == 0 ? (uint32_t)(r * H + g * 8) * 2u : (uint32_t)(r * I + g * 8) * 2u;
-  auto load_a = [&](const Meta &m, u32x4 (&buf)[NRB][AW], uint32_t (&sc)[NRB][AW]) {
+  auto load_a = [&](const Meta &m, u32x4 (&buf)[NRB][AW], ScaleT (&sc)[NRB][AW]) {
     const bool live = m.unit >= 0;
     const int ex = live ? m.expert : 0, cb = live ? m.cb : 0;
 #pragma unroll
@@ -181,6 +214,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
       load_b(mq[0]);
       // B is never in flight at a step boundary (see the task switch below).
       __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+      prep_b();
     }
   }
   int btask = mq[0].task;
@@ -197,6 +231,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
     if (cur.task != btask) {
       load_b(cur);
       __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+      prep_b();
       btask = cur.task;
     }
     f32x4 acc[NRB][MT];
@@ -204,7 +239,27 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
     for (int rb = 0; rb < NRB; ++rb) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (W4) {
+      if constexpr (FOLD) {
+#pragma unroll
+        for (int i = 0; i < AW; ++i) {
+          f32x4 tg[MT];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const u32x4 af = w4_fold8(aq[SL][rb][i][j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              tg[mt] = j == 0 ? mfma16(bfr[mt][i * 4 + j], af, f32x4{0.f, 0.f, 0.f, 0.f})
+                              : mfma16(bfr[mt][i * 4 + j], af, tg[mt]);
+          }
+          const float sc = bf16_bits_to_f32(sq[SL][rb][i]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const f32x4 xo = *(const f32x4 *)(s_xs + (wave * AWX + i) * MT * 16 + mt * 16 + 4 * g);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[rb][mt][c] = __builtin_fmaf(sc, tg[mt][c] + xo[c], acc[rb][mt][c]);
+          }
+        }
+      } else if constexpr (W4) {
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
           const W4Scale ks = w4_scale(bf16_bits_to_f32(sq[SL][rb][i]));
@@ -254,7 +309,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
       const int et = tid - ((i & 1) % (kThreads / EN)) * EN;
       if (et >= 0 && et < EN) {
         const int l = et & 63, ii = (et >> 6) & 3, mt = et >> 8;
-        const int j = mt * 16 + (l & 15);
+        // FOLD: partial tiles are [token][weight row] (token 4(l/16) + ii,
+        // feature l%16); otherwise [weight row][token].
+        const int j = FOLD ? mt * 16 + 4 * (l >> 4) + ii : mt * 16 + (l & 15);
+        const int feat = FOLD ? (l & 15) : 4 * (l >> 4) + ii;
         const float *redf = (const float *)red;
         auto part = [&](int w, int rb) { return redf[((((w * NRB + rb) * MT + mt) * 4 + ii) * kWave + l)]; };
         float sg = part(0, 0), su = part(0, 1);
@@ -267,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
         const float up = bf16_round(su);
         const float v = gt / (1.0f + expf(-gt)) * up;
         if (j < cur.rows)
-          a.act[(size_t)(cur.row0 + j) * I + cur.cb * 16 + 4 * (l >> 4) + ii] =
+          a.act[(size_t)(cur.row0 + j) * I + cur.cb * 16 + feat] =
               (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
       }
     } else {
@@ -311,10 +369,11 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ExpertArgs a) {
   }
 }
 
-template <int KIND, int MT, int SPW, bool W4>
+template <int KIND, int MT, int SPW, bool W4, bool FOLD = false>
 hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
-  auto k = stream_kernel<KIND, MT, SPW, W4>;
-  const size_t lds = (size_t)2 * kWaves * 2 * MT * kWave * sizeof(f32x4);
+  auto k = stream_kernel<KIND, MT, SPW, W4, FOLD>;
+  const size_t lds = (size_t)2 * kWaves * 2 * MT * kWave * sizeof(f32x4) +
+                     (FOLD ? (size_t)kWaves * (SPW / 4) * MT * 16 * sizeof(float) : 0);
   static int per_cu = [&] {
     int n = 1;
     (void)hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -337,6 +396,13 @@ hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStre
 template <int KIND, int MT, bool W4>
 hipError_t launch_spw(const ExpertArgs &a, int spw, int units, int num_cus, hipStream_t s) {
   if constexpr (W4) {
+    if (a.w4_fold) {
+      switch (spw) {
+        case 4: return launch_one<KIND, MT, 4, true, true>(a, units, num_cus, s);
+        case 8: return launch_one<KIND, MT, 8, true, true>(a, units, num_cus, s);
+        default: return hipErrorInvalidValue;
+      }
+    }
     switch (spw) {
       case 4: return launch_one<KIND, MT, 4, true>(a, units, num_cus, s);
       case 8: return launch_one<KIND, MT, 8, true>(a, units, num_cus, s);

@@ -143,6 +143,14 @@ def _validate_common(x, down, ids, rw, gate_up_shape):
     return e, h, inter
 
 
+def _w4_decode_mode(mode, tiled):
+    if mode not in ("exact", "fold"):
+        raise ValueError(f"w4_decode must be 'exact' or 'fold' (got {mode!r})")
+    if mode == "fold" and tiled is None:
+        raise ValueError("w4_decode='fold' needs W4G128 gate/up weights")
+    return mode
+
+
 class PreparedMoE:
     """Fixed buffers and shapes; IDs and values may change in place.
 
@@ -152,7 +160,7 @@ class PreparedMoE:
     """
 
     def __init__(self, *, x, down, ids, routing_weights, gate_up=None, tiled=None, logits=None,
-                 renormalize=True, config=None):
+                 renormalize=True, config=None, w4_decode="exact"):
         device = x.device
         e, h, inter = down.shape
         t, k = ids.shape
@@ -162,7 +170,9 @@ class PreparedMoE:
         self.output = torch.empty((t, h), dtype=torch.bfloat16, device=device)
         d = N.MoeDesc()
         d.T, d.H, d.I, d.E, d.K = t, h, inter, e, k
-        d.weight_format = N.WEIGHTS_W4G128 if tiled is not None else N.WEIGHTS_BF16
+        self.w4_decode = _w4_decode_mode(w4_decode, tiled)
+        d.weight_format = (N.WEIGHTS_BF16 if tiled is None else
+                           N.WEIGHTS_W4G128_FOLD if self.w4_decode == "fold" else N.WEIGHTS_W4G128)
         d.id_dtype = N.IDS_INT64 if ids.dtype == torch.int64 else N.IDS_INT32
         d.route_mode = N.ROUTE_LOGITS if logits is not None else N.ROUTE_FIXED
         d.renormalize = 1 if renormalize else 0
@@ -323,8 +333,13 @@ def _as_tiled(packed, device):
     raise TypeError("PackedGateUp, RepackedGateUp or TiledGateUp required")
 
 
-def prepare_w4_moe(x, packed, down, ids, routing_weights, *, down_config=None):
-    """W4A16 MoE: int4 gate/up (W4G128), bf16 down (moe_w4_cuda.py:85)."""
+def prepare_w4_moe(x, packed, down, ids, routing_weights, *, down_config=None, w4_decode="exact"):
+    """W4A16 MoE: int4 gate/up (W4G128), bf16 down (moe_w4_cuda.py:85).
+
+    ``w4_decode="exact"`` (default) multiplies the reference's dequantised
+    weights bf16_rn(q * scale); ``"fold"`` lets the about-one-row-per-expert
+    gate/up kernel apply each group's scale to the fp32 sum of its MFMAs
+    (effective weights q * scale exactly; no counterpart in the reference)."""
     e, h, inter = _validate_common(x, down, ids, routing_weights, None)
     tiled = _as_tiled(packed, x.device)
     if tuple(tiled.shape) != (e, 2 * inter, h):
@@ -332,7 +347,7 @@ def prepare_w4_moe(x, packed, down, ids, routing_weights, *, down_config=None):
     _device_check({"down": down, "ids": ids, "routing_weights": routing_weights, "x": x,
                    "words": tiled.words, "scales": tiled.scales}, x.device)
     plan = PreparedMoE(x=x, tiled=tiled, down=down, ids=ids, routing_weights=routing_weights,
-                       config=down_config)
+                       config=down_config, w4_decode=w4_decode)
     plan.run()
     return plan
 
@@ -363,7 +378,7 @@ class PreparedRoutedMoE(PreparedMoE):
 
 
 def prepare_routed_moe(hidden, router_logits, gate_up, down, top_k, *, renormalize=True,
-                       config=None):
+                       config=None, w4_decode="exact"):
     """Prepare the full MoE forward.  ``gate_up`` is a bf16 [E,2I,H] tensor or
     a PackedGateUp / TiledGateUp (W4A16).  ``hidden`` and ``router_logits`` are
     bound by address; ``forward`` copies other tensors into them."""
@@ -390,6 +405,6 @@ def prepare_routed_moe(hidden, router_logits, gate_up, down, top_k, *, renormali
         config, _ = FrozenMoEPolicy().select(t, e, top_k, h, inter)
     plan = PreparedRoutedMoE(x=hidden, gate_up=gate_up, tiled=tiled, down=down, ids=ids,
                              routing_weights=rw, logits=router_logits, renormalize=renormalize,
-                             config=config)
+                             config=config, w4_decode=w4_decode)
     plan.run()
     return plan

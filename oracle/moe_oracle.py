@@ -263,6 +263,18 @@ def dequantize_w4(words, scales):
     return (q * scales.float()[..., None]).reshape(e, n, kw * 8).to(torch.bfloat16)
 
 
+def dequantize_w4_unrounded(words, scales):
+    """float(nibble - 8) * float(scale) in fp32, not rounded to bf16: the
+    effective weights of the opt-in folded decode (no counterpart in the
+    reference).  Exact: an int4 times an 8-bit-significand scale has at most
+    12 significant bits; rounding it to bf16 gives dequantize_w4."""
+    e, n, kw = words.shape
+    shifts = torch.arange(8, dtype=torch.int64) * 4
+    nib = (words.to(torch.int64)[..., None] >> shifts) & 15
+    q = (nib.reshape(e, n, kw * 8 // W4_GROUP, W4_GROUP) - 8).float()
+    return (q * scales.float()[..., None]).reshape(e, n, kw * 8)
+
+
 def m24_repack(words, scales):
     """v1 -> M24 physical layout, the reference's permutation
     (src/llm_gpu_kernels/moe_weight_layout.py:85-88, LAYOUT at :14-17 with

@@ -88,6 +88,8 @@ def test_layout_for_qwen_shape():
     assert lay.launches == 3
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, fmt=N.WEIGHTS_W4G128))
     assert lay.launches == 4  # W4: router fused into the planner
+    rc2, lay2 = _layout(_desc(route=N.ROUTE_LOGITS, T=17, fmt=N.WEIGHTS_W4G128_FOLD))
+    assert rc2 == 0 and (lay2.total, lay2.launches, lay2.fast_path) == (lay.total, lay.launches, lay.fast_path)
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, H=4096))
     assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=33))
@@ -103,6 +105,7 @@ def test_layout_for_qwen_shape():
                                 dict(route=N.ROUTE_LOGITS, ids=N.IDS_INT64),
                                 dict(route=N.ROUTE_LOGITS, E=4, K=8),
                                 dict(fmt=N.WEIGHTS_W4G128, H=192), dict(fmt=N.WEIGHTS_W4G128, H=512, I=48),
+                                dict(fmt=N.WEIGHTS_W4G128_FOLD, H=192), dict(fmt=3),
                                 dict(T=2 ** 27, K=16)])
 def test_layout_rejects_invalid_descriptors(kw):
     rc, _ = _layout(_desc(**kw))

@@ -192,6 +192,34 @@ def test_routed_w4_layer(tokens, gpu_device):
     _routed_parity("qwen", tokens, "uniform", gpu_device, w4=True)
 
 
+@pytest.mark.parametrize("tokens", [17, 193, 1024])
+def test_routed_w4_fold_layer(tokens, gpu_device):
+    """Opt-in folded W4 decode (group scale on the fp32 group sum): within
+    tolerance of the FP32 oracle on the unrounded q * scale weights, router IDs
+    bit-exact, bitwise repeatable; at T = 17 (the split-K streaming kernel that
+    implements the fold) it differs from the exact decode's output."""
+    lay = make_layer("qwen", tokens, seed=0, device=gpu_device)
+    packed = quantize_gate_up(lay["gate_up"].cpu())
+    tiled = tile_gate_up(packed).to(gpu_device)
+    plan = prepare_routed_moe(lay["x"], lay["logits"], tiled, lay["down"], lay["K"], w4_decode="fold")
+    out = plan.forward(lay["x"], lay["logits"]).clone()
+    again = plan.forward(lay["x"], lay["logits"]).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    ids, w = O.route_topk(lay["logits"].cpu(), lay["K"])
+    assert torch.equal(plan.ids.cpu(), ids)
+    un = O.dequantize_w4_unrounded(packed.words, packed.scales)
+    m = O.error(out, O.moe_reference(lay["x"].cpu(), un, lay["down"].cpu(), ids, w))
+    assert m["passed"], m
+    if tokens == 17:
+        exact = prepare_routed_moe(lay["x"], lay["logits"], tiled, lay["down"], lay["K"])
+        ex = exact.forward(lay["x"], lay["logits"])
+        torch.cuda.synchronize()
+        assert not torch.equal(ex.view(torch.int16), out.view(torch.int16))
+    with pytest.raises(ValueError):
+        prepare_routed_moe(lay["x"], lay["logits"], tiled, lay["down"], lay["K"], w4_decode="bf16")
+
+
 # One GPU's share of the Qwen layer under 8-way expert parallelism (16 experts,
 # one route per row: the streaming and the tiled kernels) and tensor parallelism
 # (I = 96: the run-time-K kernels), as the bench measures them.

@@ -212,6 +212,29 @@ def test_w4_round_trip_error_bound():
     assert torch.equal(w2, words)
 
 
+def test_w4_unrounded_dequantisation():
+    """The folded decode's effective weights: q * scale exactly in fp32.  Closed
+    forms (scale 3 * 2^-3 = 0.375: q * s needs up to 5 significant bits, so
+    nothing rounds; scale 1 + 2^-7: 7 * s = 7 + 7/128 has 10 significant bits
+    and rounds in bf16), and rounding to bf16 gives dequantize_w4 bitwise."""
+    q = torch.tensor([-8, -7, -3, 0, 1, 3, 5, 7])
+    word = int(sum((int(v) + 8) << (4 * i) for i, v in enumerate(q.tolist())))
+    words = torch.tensor([[[word - 2 ** 32 if word >= 2 ** 31 else word] * 16]], dtype=torch.int32)
+    for sc in (0.375, 1 + 2 ** -7):
+        scales = torch.tensor([[[sc]]], dtype=torch.bfloat16)
+        un = O.dequantize_w4_unrounded(words, scales)
+        assert un[0, 0, :8].tolist() == [float(v) * sc for v in q.tolist()]
+        assert torch.equal(un.to(torch.bfloat16), O.dequantize_w4(words, scales))
+    assert O.dequantize_w4_unrounded(words, torch.tensor([[[1 + 2 ** -7]]], dtype=torch.bfloat16))[0, 0, 7] \
+        != O.dequantize_w4(words, torch.tensor([[[1 + 2 ** -7]]], dtype=torch.bfloat16))[0, 0, 7].float()
+    g = torch.Generator().manual_seed(9)
+    w = (torch.randn((2, 16, 512), generator=g) * 0.02).to(torch.bfloat16)
+    words, scales = O.quantize_w4(w)
+    un, deq = O.dequantize_w4_unrounded(words, scales), O.dequantize_w4(words, scales)
+    assert torch.equal(un.to(torch.bfloat16), deq)
+    assert ((un - deq.float()).abs() <= un.abs() * 2 ** -8).all()  # bf16 unit roundoff
+
+
 def test_gqa_reference_matches_manual_softmax():
     g = torch.Generator().manual_seed(0)
     t, hq, hkv, d = 3, 4, 2, 8
