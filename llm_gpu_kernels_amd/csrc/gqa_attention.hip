@@ -102,6 +102,7 @@ constexpr float kRescaleSlack = 8.f;
 struct Tile {
   int n;            // valid rows (1..32)
   int local0;       // index of the first key within its segment
+  int send;         // global end of the tile's segment
   bool causal;      // the keys lie in the current (causal) segment
   const uint8_t *kb, *vb;  // row 0 (KV head offset included)
   uint32_t ksb, vsb;       // token strides in bytes (32 * stride < 2^31, checked on the host)
@@ -169,6 +170,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
     const int send = seg == 0 ? st1 : seg == 1 ? st2 : seg == 2 ? st3 : INT_MAX;
     t.n = min(kKC, min(send, k_end) - pos);
     t.local0 = pos - sbeg;
+    t.send = send;
     t.causal = seg == nseg - 1;
     // seg is wave-uniform, so these are scalar loads of the kernel arguments.
     const int64_t ks = a.k_stride[seg], vs = a.v_stride[seg];
@@ -258,8 +260,22 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) *(u32x4 *)(stage + k_off(4 * i + g, r)) = vn[i];
     const int next = pos + cur.n;
-    const Tile nxt = tile_at(next);
+    // Within a segment the next tile only advances the row pointers; the
+    // segment's pointers and strides (dynamically indexed kernel arguments,
+    // a scalar memory round trip) are read only when a step crosses into
+    // the next segment.
     const bool more = next < k_end;
+    Tile nxt = cur;
+    if (!more) {
+      // the last step: no next tile
+    } else if (next < cur.send) {
+      nxt.n = min(kKC, min(cur.send, k_end) - next);
+      nxt.local0 = cur.local0 + cur.n;
+      nxt.kb = cur.kb + (size_t)cur.n * cur.ksb;
+      nxt.vb = cur.vb + (size_t)cur.n * cur.vsb;
+    } else {
+      nxt = tile_at(next);
+    }
     if (more) load_v(nxt);
 
     // S^T: lane holds keys 16*kt + 4g + i of token r, per row block.
