@@ -55,6 +55,10 @@ class PreparedSegmentedGQA:
     def __init__(self, q, segments, out=None, scale=None):
         if not isinstance(q, torch.Tensor) or q.ndim != 3 or q.shape[2] != 128:
             raise ValueError("q must be [T, Hq, 128]")
+        if scale is not None and not (math.isfinite(float(scale)) and float(scale) > 0.0):
+            # the C ABI reads a scale <= 0 or non-finite as "default"; an explicit
+            # one must not be replaced silently
+            raise ValueError(f"scale must be a positive finite number (got {scale!r})")
         if q.dtype != torch.bfloat16 or not q.is_contiguous() or q.device.type != "cuda":
             raise ValueError("q must be a contiguous bf16 GPU tensor")
         segments = [tuple(s) for s in segments]

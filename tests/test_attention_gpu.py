@@ -112,6 +112,9 @@ def test_rejects_bad_inputs(gpu_device):
         prepare_segmented_gqa(q, segs[:-1] + [(segs[-1][0][:4], segs[-1][1][:4])])
     with pytest.raises(TypeError):
         prepare_segmented_gqa(q, [(k.float(), v) for k, v in segs])
+    for bad in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(ValueError):
+            prepare_segmented_gqa(q, segs, scale=bad)
 
 
 def test_out_aliasing_rejected(gpu_device):
