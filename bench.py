@@ -38,6 +38,7 @@ WORKLOADS = {
     # The opt-in folded W4 decode (group scale on the fp32 group sum; effective
     # weights q * scale, not the reference's bf16_rn(q * scale)).
     "qwen-w4fold-t17": dict(shape="qwen", T=17, routing="uniform", w4=True, fold=True),
+    "qwen-w4fold-t193": dict(shape="qwen", T=193, routing="uniform", w4=True, fold=True),
     "tiny-bf16-t17": dict(shape="tiny", T=17, routing="uniform", w4=False),
     # One GPU's share of the Qwen layer under 8-way expert / tensor parallelism
     # (the local kernels at their real shard shapes; no collectives).

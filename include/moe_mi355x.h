@@ -54,7 +54,7 @@ extern "C" {
 #define MOE_WEIGHTS_W4G128 1      /* gate_up int4 in the tiled layout below;  *
                                    * needs H % 128 == 0 and I % 32 == 0        */
 /* The same W4G128 weights, opt-in folded decode: where a kernel implements it
- * (the split-K streaming gate/up of the about-one-row-per-expert regime), the
+ * (the split-K streaming gate/up, used in this mode for 16- and 32-row tasks), the
  * MFMAs run on the exact values 136 + q and each 128-K group's fp32 sum is
  * scaled after subtracting 136 x the group's token sums, i.e. the effective
  * weights are q * scale exactly instead of bf16_rn(q * scale) (no counterpart
