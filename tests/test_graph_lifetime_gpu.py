@@ -36,20 +36,24 @@ FAMILIES = [
     ("w4-t17-stream", 17, "uniform", True, 4),                # W4 register-streaming gate/up
     ("w4-t193-wave", 193, "uniform", True, 4),                # W4 one-unit-per-wave gate/up
     ("w4-t1024-wave", 1024, "uniform", True, 4),              # W4 wave gate/up, 64-row tasks
+    ("w4fold-t17-stream", 17, "uniform", "fold", 4),          # folded decode, split-K streaming
+    ("w4fold-t193-stream", 193, "uniform", "fold", 4),        # folded decode, 16-row tasks
 ]
 
 _WEIGHTS = {}
 
 
 def _weights(w4, device):
-    """Qwen-shape weights, built once per module (bf16 and their W4 tiling)."""
-    key = "w4" if w4 else "bf16"
+    """Qwen-shape weights, built once per module (bf16 and their W4 tiling; with
+    w4 == "fold" the oracle gets the unrounded q * scale weights)."""
+    key = "w4fold" if w4 == "fold" else "w4" if w4 else "bf16"
     if key not in _WEIGHTS:
         lay = make_layer("qwen", 1, seed=0, device=device)
         if w4:
             packed = quantize_gate_up(lay["gate_up"].cpu())
             tiled = tile_gate_up(packed).to(device)
-            _WEIGHTS[key] = (tiled, O.dequantize_w4(packed.words, packed.scales), lay["down"])
+            ref = (O.dequantize_w4_unrounded if w4 == "fold" else O.dequantize_w4)(packed.words, packed.scales)
+            _WEIGHTS[key] = (tiled, ref, lay["down"])
         else:
             _WEIGHTS[key] = (lay["gate_up"], lay["gate_up"].cpu(), lay["down"])
     return _WEIGHTS[key]
@@ -100,7 +104,8 @@ def test_routed_graph_replays(name, tokens, routing, w4, launches, gpu_device):
     gate_up, ref_gu, down = _weights(w4, gpu_device)
     lay = make_layer("qwen", tokens, routing=routing, seed=tokens, device=gpu_device,
                      weights=False)
-    plan = prepare_routed_moe(lay["x"], lay["logits"], gate_up, down, 8)
+    plan = prepare_routed_moe(lay["x"], lay["logits"], gate_up, down, 8,
+                              w4_decode="fold" if w4 == "fold" else "exact")
     assert len(plan.launches) == launches, plan.launch_names
     nexts = []
     for step in range(3):
