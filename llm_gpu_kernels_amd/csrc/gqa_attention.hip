@@ -29,6 +29,7 @@
 // also split across workgroups and a second kernel merges the partial states
 // in fixed split order (gqa_shape).
 #include <climits>
+#include <type_traits>
 #include "common.h"
 #include "gqa_internal.h"
 
@@ -63,15 +64,52 @@ __device__ __forceinline__ V gload_as(const void *p) {
   return *(const GQA_GLOBAL V *)(const GQA_GLOBAL void *)p;
 }
 
-// Byte offset of 16-byte chunk c of row r in a row-major tile of 256-byte rows
-// (128 bf16), chunks XOR-swizzled by the row's low four bits.
-__device__ __forceinline__ int k_off(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
-
+// LDS reads of the stages that the buffer loads with an LDS destination
+// fill, written as inline assembly: the compiler cannot tell which of those
+// loads a read depends on and would wait for all of them, including the
+// next step's.  The reads are only issued here; lds_wait() completes them
+// and hands the registers on (the "+v" operands keep every use of them
+// after it), and the kernel waits for the loads with exact counts itself.
+// `off` is a compile-time byte offset.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
+  return (uint32_t)(uintptr_t)(const GQA_LDS uint8_t *)p;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_issue_b128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane 4a+b receives
 // element b of the 8-byte rows addressed by lanes a, a+4, a+8, a+12.
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint8_t *lds, int byte_off) {
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GQA_LDS i16x4 *)(lds + byte_off));
-  return __builtin_bit_cast(u32x2, v);
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_issue_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_wait(u32x2 (&v)[16]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
+                 "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15])
+               :
+               : "memory");
+}
+__device__ __forceinline__ void lds_wait(u32x4 (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+               :
+               : "memory");
+}
+
+// 16 bytes per lane from a buffer straight into LDS (lane l's bytes at
+// dst + 16 l); lanes whose offset is past the descriptor's size read zero.
+// The builtin is compiled in the device pass only: in the host pass a kernel
+// that calls it loses its launch stub.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GQA_LDS void *)dst, 16, off, 0, 0, 0);
+#endif
 }
 
 // Reductions over the four 16-lane rows holding one token's keys (lanes
@@ -100,7 +138,8 @@ constexpr float kRescaleSlack = 8.f;
 // the row addresses are (segment base) + row * (segment stride) with
 // wave-uniform base and stride.
 struct Tile {
-  int n;            // valid rows (1..32)
+  int pos;          // global index of the first key
+  int n;            // valid rows (1..32; 0 = past the wave's last key)
   int local0;       // index of the first key within its segment
   int send;         // global end of the tile's segment
   bool causal;      // the keys lie in the current (causal) segment
@@ -128,11 +167,20 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
   constexpr int kWaves = NW;
   constexpr int kRB = RB;
   constexpr int QT = 16 * (kRB / HPW);                 // tokens per workgroup
-  constexpr int kStage = kKC * kD * 2;                 // V staging per wave (8 KB)
-  constexpr int kOBytes = kWaves * kRB * 8 * 64 * 16;  // merge: O states (8 KB per wave and row block)
-  constexpr int kMLBytes = kWaves * kRB * 16 * 2 * 4;  // merge: (m, l) per row
-  static_assert(kWaves * kStage <= kOBytes, "V staging aliases the merge area");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kOBytes + kMLBytes];
+  constexpr int kVBlock = 4 * kD * 2 + 32;             // V stage block: four rows + pad
+  constexpr int kStage = 8 * kVBlock;                  // V stage per wave (8.25 KiB)
+  // LDS: per wave one K stage and one V stage.  The merge after the loop
+  // reuses them: O states of row block 0 in the K array, of row block 1 in
+  // the V array, (m, l) after the O states in the K array.
+  constexpr int kKBlock = 8 * 128 + 64;                // K stage block: 8 keys x 128 bytes + pad
+  constexpr int kKStage = 8 * kKBlock;
+  constexpr int kOBytes = kWaves * 8 * 64 * 16;        // O states of one row block
+  constexpr int kMLBytes = kWaves * kRB * 16 * 2 * 4;  // (m, l) per row
+  static_assert(kRB <= 2 && kOBytes <= kWaves * kStage && kOBytes <= kWaves * kKStage,
+                "O states fit the stage arrays");
+  static_assert(kOBytes + kMLBytes <= kWaves * kKStage, "(m, l) fit after the O states");
+  __shared__ __attribute__((aligned(16))) uint8_t kst[kWaves * kKStage];
+  __shared__ __attribute__((aligned(16))) uint8_t vst[kWaves * kStage];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = sgpr(tid >> 6);
@@ -168,7 +216,8 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
     const int seg = sgpr((pos >= st1) + (pos >= st2) + (pos >= st3));
     const int sbeg = seg == 0 ? 0 : seg == 1 ? st1 : seg == 2 ? st2 : st3;
     const int send = seg == 0 ? st1 : seg == 1 ? st2 : seg == 2 ? st3 : INT_MAX;
-    t.n = min(kKC, min(send, k_end) - pos);
+    t.pos = pos;
+    t.n = max(0, min(kKC, min(send, k_end) - pos));
     t.local0 = pos - sbeg;
     t.send = send;
     t.causal = seg == nseg - 1;
@@ -182,7 +231,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
   };
 
   // Q fragments (B operand of S^T = K Q^T): lane l -> token l%16 of the row
-  // block, dims 32*ks + 8*(l/16) .. +8.
+  // block, dims 32*ks + 8*(l/16) .. +8; rows past T repeat row T - 1.
   u32x4 qf[kRB][4];
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
@@ -206,101 +255,115 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
   }
   const float sl2 = a.scale * kLog2e;
 
-  // Register prefetch.  K: A-operand fragments, lane l -> key 16*kt + l%16,
-  // dims 32*ks + 8*(l/16).  V: whole 256-byte rows, 16 lanes per row.  Rows
-  // past the step's end re-read row 0 (masked out below).  The next step's V
-  // is requested as soon as this step's V is in LDS, the next step's K as soon
-  // as this step's score MFMAs have read their K fragments, so one register
-  // set of each suffices.
-  u32x4 kf[2][4], vn[8];
-  // Addresses are a scalar row base plus one per-lane offset per tile, with
-  // the column offset in the instruction's immediate field; only a partial
-  // tile (rows past its end clamp to its last row) needs per-row lane math.
-  auto load_k = [&](const Tile &t) __attribute__((always_inline)) {
-    if (t.n == kKC) {
-      const uint32_t lo = r * t.ksb + 16 * g;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kf[kt][ks] = gload_as<u32x4>(t.kb + 16 * kt * t.ksb + lo + 64 * ks);
-    } else {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const uint32_t off = min(16 * kt + r, t.n - 1) * t.ksb + 16 * g;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kf[kt][ks] = gload_as<u32x4>(t.kb + off + 64 * ks);
-      }
-    }
+  // K and V of the next step are loaded while this one computes, straight
+  // into the wave's LDS stages (buffer loads with an LDS destination: lane l
+  // of a load writes 16 bytes at the stage block + 16 l).  Every load goes
+  // through a buffer descriptor bounded at the tile's n rows, so rows past a
+  // partial tile read as zero (masked out below) and a tile past the wave's
+  // last key (n = 0) reads nothing -- but still issues its loads, so the
+  // number of loads in flight after any given one is fixed and the waits
+  // below are exact counts.
+  u32x4 vb[8];
+  // (The tile fields are wave-uniform; readfirstlane states it, so the
+  // descriptor lives in scalar registers and no load is split per lane.)
+  auto rsrc = [&](const uint8_t *base, uint32_t bytes) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)sgpr64((uint64_t)base), (short)0, sgpr((int)bytes), 0x00020000);
   };
-  auto load_v = [&](const Tile &t) __attribute__((always_inline)) {
-    if (t.n == kKC) {
-      const uint32_t lo = g * t.vsb + 16 * r;
+  // K stage: load j (block j, kKBlock bytes apart) reads keys 8(j/2) .. +7,
+  // bytes 128(j%2) .. +127 of each -- eight lanes per 128-byte line, so
+  // every cache line is read whole -- with the eight 16-byte chunks of key k
+  // permuted by k%8: lane l takes key 8(j/2) + l/8, chunk (l%8) ^ (l/8).
+  auto issue_k = [&](const Tile &t, uint8_t *stage) __attribute__((always_inline)) {
+    const auto rs = rsrc(t.kb, (uint32_t)t.n * t.ksb);
+    const uint32_t lo = (uint32_t)(lane >> 3) * t.ksb + 16 * ((lane & 7) ^ (lane >> 3));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vn[i] = gload_as<u32x4>(t.vb + 4 * i * t.vsb + lo);
+    for (int j = 0; j < 8; ++j)
+      buffer_load_lds16(rs, stage + j * kKBlock, lo + (uint32_t)(8 * (j >> 1)) * t.ksb + 128 * (j & 1));
+  };
+  // A-operand fragment (kt, ks) of S^T -- lane (r, g) needs key 16kt + r,
+  // chunk c = 4ks + g -- sits in block 4kt + 2(r/8) + ks/2 at 16-byte slot
+  // 8(r%8) + (c%8 ^ r%8); c%8 ^ r%8 = (g ^ r%8) ^ 4(ks%2).  The sixteen
+  // lanes of one g then read sixteen different 16-byte bank groups (the
+  // blocks of keys r and r + 8 are 2 kKBlock = 128 (mod 256) bytes apart).
+  const int kx = r & 7;
+  const uint32_t kbase0 = (uint32_t)(2 * kKBlock * (r >> 3) + 128 * kx + 16 * (g ^ kx));
+  const uint32_t kbase1 = (uint32_t)(2 * kKBlock * (r >> 3) + 128 * kx + 16 * ((g ^ kx) ^ 4));
+  // V stage layout: block b (0..7, kVBlock bytes apart) holds keys b, b + 8,
+  // b + 16, b + 24 as four 256-byte rows.  The transposed reads of a 16-lane
+  // group then touch four blocks whose 32-byte pad puts their rows in
+  // different banks, and every read address is one per-lane base plus an
+  // immediate.
+  auto issue_v = [&](const Tile &t, uint8_t *stage) __attribute__((always_inline)) {
+    const auto rs = rsrc(t.vb, (uint32_t)t.n * t.vsb);
+    const uint32_t lo = (uint32_t)(8 * g) * t.vsb + 16 * r;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+      buffer_load_lds16(rs, stage + b * kVBlock, lo + b * t.vsb);
+  };
+  // The tile after t: within a segment only the row pointers advance; the
+  // segment's pointers and strides (dynamically indexed kernel arguments, a
+  // scalar memory round trip) are read only when crossing into the next one.
+  auto next_tile = [&](const Tile &t) __attribute__((always_inline)) {
+    const int p = t.pos + t.n;
+    Tile u = t;
+    if (t.n == 0 || p >= k_end) {
+      u.n = 0;
+    } else if (p < t.send) {
+      u.pos = p;
+      u.n = min(kKC, min(t.send, k_end) - p);
+      u.local0 = t.local0 + t.n;
+      u.kb = t.kb + (size_t)t.n * t.ksb;
+      u.vb = t.vb + (size_t)t.n * t.vsb;
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        vn[i] = gload_as<u32x4>(t.vb + (min(4 * i + g, t.n - 1) * t.vsb + 16 * r));
+      u = tile_at(p);
     }
+    return u;
   };
 
-  uint8_t *stage = smem + wave * kStage;
-  // B operand of P.V from the staged V rows: lane l (group g = l/16,
-  // a = l%4, j = (l%16)/4) addresses row 16h + 4g + j, dims 16dt + 4a .. +3;
-  // after the transpose lane l holds dim 16dt + l%16 of keys 16h + 4g + 0..3.
-  const int tr_row = 4 * g + (r >> 2), tr_a = r & 3;
+  // B operand of P.V from the staged V rows: lane (g, j = (l%16)/4,
+  // a = l%4) reads key 4g + j -- block 4(g&1) + j, row g/2 -- at dims
+  // 16dt + 4a .. +3, and key 16 + 4g + j two rows further; after the
+  // transpose lane l holds dim 16dt + l%16 of keys 4g + 0..3 (+ 16).
+  const uint32_t tr_base = (uint32_t)((4 * (g & 1) + (r >> 2)) * kVBlock + (g >> 1) * 256 + 8 * (r & 3));
+  uint8_t *const kstage = kst + wave * kKStage;
+  uint8_t *const vstage = vst + wave * kStage;
 
-  int pos = k_beg;
-  Tile cur = tile_at(pos);
-  if (pos < k_end) {
-    load_k(cur);
-    load_v(cur);
-  }
-  while (pos < k_end) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) *(u32x4 *)(stage + k_off(4 * i + g, r)) = vn[i];
-    const int next = pos + cur.n;
-    // Within a segment the next tile only advances the row pointers; the
-    // segment's pointers and strides (dynamically indexed kernel arguments,
-    // a scalar memory round trip) are read only when a step crosses into
-    // the next segment.
-    const bool more = next < k_end;
-    Tile nxt = cur;
-    if (!more) {
-      // the last step: no next tile
-    } else if (next < cur.send) {
-      nxt.n = min(kKC, min(cur.send, k_end) - next);
-      nxt.local0 = cur.local0 + cur.n;
-      nxt.kb = cur.kb + (size_t)cur.n * cur.ksb;
-      nxt.vb = cur.vb + (size_t)cur.n * cur.vsb;
-    } else {
-      nxt = tile_at(next);
-    }
-    if (more) load_v(nxt);
-
+  Tile cur = tile_at(k_beg), nx = next_tile(cur);
+  issue_k(cur, kstage);
+  issue_v(cur, vstage);
+  while (cur.n > 0) {
+    // This step's K has landed once at most the 8 loads of its V remain.
+    __builtin_amdgcn_s_waitcnt((8 & 15) | ((8 >> 4) << 14) | (7 << 4) | (15 << 8));
     // S^T: lane holds keys 16*kt + 4g + i of token r, per row block.
     f32x4 s[kRB][2];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) s[rb][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Fragment (kt, ks) -> kf[2 ks + kt].
+    u32x4 kf[8];
+    {
+      const uint32_t ka0 = lds_addr(kstage) + kbase0, ka1 = lds_addr(kstage) + kbase1;
+      kf[0] = lds_issue_b128<0 * kKBlock>(ka0);
+      kf[1] = lds_issue_b128<4 * kKBlock>(ka0);
+      kf[2] = lds_issue_b128<0 * kKBlock>(ka1);
+      kf[3] = lds_issue_b128<4 * kKBlock>(ka1);
+      kf[4] = lds_issue_b128<1 * kKBlock>(ka0);
+      kf[5] = lds_issue_b128<5 * kKBlock>(ka0);
+      kf[6] = lds_issue_b128<1 * kKBlock>(ka1);
+      kf[7] = lds_issue_b128<5 * kKBlock>(ka1);
+      lds_wait(kf);
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) s[rb][kt] = mfma16(kf[kt][ks], qf[rb][ks], s[rb][kt]);
-    if (more) load_k(nxt);
-
-    u32x4 vb[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int c = 2 * dt + (tr_a >> 1), w = 8 * (tr_a & 1);
-      const u32x2 lo = lds_read_tr16(stage, k_off(tr_row, c) + w);
-      const u32x2 hi = lds_read_tr16(stage, k_off(16 + tr_row, c) + w);
-      vb[dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-    }
-
+        for (int kt = 0; kt < 2; ++kt) s[rb][kt] = mfma16(kf[2 * ks + kt], qf[rb][ks], s[rb][kt]);
+    // The K stage is refilled only after every read of it has returned
+    // (lds_wait above: the LDS-destination loads do not queue behind this
+    // wave's LDS reads).
+    issue_k(nx, kstage);
     const bool full = cur.n == kKC && !cur.causal;
     // Mask (raw scores): rows past the step's end and, in the current
     // segment, keys after the token (key j of the current chunk is token j).
@@ -349,6 +412,31 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
           for (int i = 0; i < 4; ++i) o[rb][dt][i] *= al[i];
       }
     }
+    // V is read after the rare rescale branch, so its 32 registers are not
+    // live across it; the exponentials below cover the reads' latency.
+    // This step's V has landed once at most the 8 loads of the next K remain.
+    __builtin_amdgcn_s_waitcnt((8 & 15) | ((8 >> 4) << 14) | (7 << 4) | (15 << 8));
+    // vr[2 dt] = dims 16dt.. of keys 4g + 0..3, vr[2 dt + 1] = keys 16 + 4g + 0..3.
+    u32x2 vr[16];
+    {
+      const uint32_t va = lds_addr(vstage) + tr_base;
+      vr[0] = lds_issue_tr16<0>(va);
+      vr[1] = lds_issue_tr16<512>(va);
+      vr[2] = lds_issue_tr16<32>(va);
+      vr[3] = lds_issue_tr16<544>(va);
+      vr[4] = lds_issue_tr16<64>(va);
+      vr[5] = lds_issue_tr16<576>(va);
+      vr[6] = lds_issue_tr16<96>(va);
+      vr[7] = lds_issue_tr16<608>(va);
+      vr[8] = lds_issue_tr16<128>(va);
+      vr[9] = lds_issue_tr16<640>(va);
+      vr[10] = lds_issue_tr16<160>(va);
+      vr[11] = lds_issue_tr16<672>(va);
+      vr[12] = lds_issue_tr16<192>(va);
+      vr[13] = lds_issue_tr16<704>(va);
+      vr[14] = lds_issue_tr16<224>(va);
+      vr[15] = lds_issue_tr16<736>(va);
+    }
     u32x4 pa[kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
@@ -365,26 +453,39 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
       pa[rb] = u32x4{pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
                      pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
     }
+    // The reads complete (and the stage may be refilled) once the
+    // exponentials above have covered their latency.
+    lds_wait(vr);
+    issue_v(nx, vstage);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) vb[dt] = u32x4{vr[2 * dt][0], vr[2 * dt][1], vr[2 * dt + 1][0], vr[2 * dt + 1][1]};
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) o[rb][dt] = mfma16(pa[rb], vb[dt], o[rb][dt]);
-    pos = next;
-    cur = nxt;
+    cur = nx;
+    nx = next_tile(nx);
   }
+  // The last issued loads (of empty tiles) may still be in flight; the merge
+  // below reuses the stages.
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) l_run[rb] = rows_sum(l_run[rb]);
 
   // Merge of the waves' states, fixed wave order.  The staging areas
   // are reused, so every wave must be past its loop first.
-  float *ost = (float *)smem;               // [wave][rb][dt][lane] x 4
-  float *ml = (float *)(smem + kOBytes);    // [wave][rb][row] x {m, l}
+  // O states of row block rb: [wave][dt][lane] x 4 at ost(rb); (m, l):
+  // [wave][rb][row].
+  auto ost = [&](int rb) __attribute__((always_inline)) {
+    return (float *)(rb ? vst : kst);
+  };
+  float *ml = (float *)(kst + kOBytes);
   __syncthreads();
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) *(f32x4 *)(ost + (((wave * kRB + rb) * 8 + dt) * 64 + lane) * 4) = o[rb][dt];
+    for (int dt = 0; dt < 8; ++dt) *(f32x4 *)(ost(rb) + ((wave * 8 + dt) * 64 + lane) * 4) = o[rb][dt];
     if (g == 0) *(f32x2_t *)(ml + ((wave * kRB + rb) * 16 + r) * 2) = f32x2_t{m_run[rb], l_run[rb]};
   }
   __syncthreads();
@@ -417,7 +518,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 4 / RB) void gqa_fwd_kernel(
     acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int src = 0; src < kWaves; ++src) {
-      const f32x4 v = *(const f32x4 *)(ost + (((src * kRB + rb) * 8 + dt0 + j) * 64 + lane) * 4);
+      const f32x4 v = *(const f32x4 *)(ost(rb) + ((src * 8 + dt0 + j) * 64 + lane) * 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][i] += wgt[src][i] * v[i];
     }
