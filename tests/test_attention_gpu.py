@@ -106,6 +106,23 @@ def test_graph_replay_and_stream(gpu_device):
         _check(replay, q, segs)
 
 
+@pytest.mark.parametrize("tokens", [32, 96])
+def test_split_runs_repeat_bitwise(tokens, gpu_device):
+    """Key-split shapes (T = 32: eight splits, T = 96: two on 256 CUs):
+    repeated runs of one plan merge the partial states in the same fixed order,
+    so they give bitwise the same output."""
+    q, segs = _values(21 + tokens, tokens, (1024, 512, 256), gpu_device)
+    plan = prepare_segmented_gqa(q, segs)
+    torch.cuda.synchronize()
+    assert plan.splits_workspace_bytes > 0
+    first = plan.output.clone()
+    _check(first, q, segs)
+    for _ in range(4):
+        plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(plan.output.view(torch.int16), first.view(torch.int16))
+
+
 def test_rejects_bad_inputs(gpu_device):
     q, segs = _values(1, 8, (4, 0, 2), gpu_device)
     with pytest.raises(ValueError):
