@@ -599,10 +599,10 @@ int gqa_heads_per_wg(int G) { return G < kLaunchRB ? G : kLaunchRB; }
 // them for two per CU: four-wave workgroups, no split.  Otherwise eight-wave
 // workgroups, one per CU (the same two waves per SIMD, keys split eight ways
 // inside the workgroup and merged in LDS), and the keys are split across
-// workgroups only as many times as fills the CUs without starting a second,
-// partial round of workgroups (rounding the split count up measured 5 us
-// slower at T = 96); with one workgroup per CU or more there is no merge
-// launch at all.
+// workgroups half as many times as would fill the CUs: the merge launch and
+// its partial states cost more than the idle CUs (on 256 CUs, T = 32: four
+// splits 14.2 us, eight 15.2, two 15.5, none 16.8; T = 96: none 17.8 us, two
+// 18.3).  With one workgroup per CU or more there is no merge launch at all.
 GqaShape gqa_shape(int T, int Hq, int Hkv, int num_cus) {
   const int G = Hq / Hkv, hpw = gqa_heads_per_wg(G);
   const int qt = 16 * (kLaunchRB / hpw);
@@ -612,7 +612,7 @@ GqaShape gqa_shape(int T, int Hq, int Hkv, int num_cus) {
   if (wgs >= num_cus * per_cu) return {1, 4};
   const int waves = kLaunchRB == 2 ? 8 : 4;
   const int slots = waves == 8 ? num_cus : num_cus * per_cu;
-  int s = slots / wgs;
+  int s = slots / wgs / 2;
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
   return {s, waves};
