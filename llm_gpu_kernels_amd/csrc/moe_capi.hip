@@ -102,11 +102,17 @@ int validate(const moe_desc *d) {
   return MOE_OK;
 }
 
-// Router-fused bf16 shapes whose gate/up streams through LDS with 16-row
-// tasks plan in the gate/up prologue instead of a planner launch.
+// Router-fused shapes with 16-row tasks whose gate/up is a streaming kernel
+// (bf16 through LDS, W4 straight into registers) plan in the gate/up prologue
+// instead of a planner launch.  W4 shapes that take the decode-once wave
+// kernel (R >= 4E, exact decode) keep the planner launch.
 bool planned_gate_up(const moe_desc *d, int path, int tb) {
-  return path == moe::kStream && tb == 16 && !is_w4(d->weight_format) &&
-         moe::dma_plan_ok(d->H, d->I, d->T, d->K, d->E, fuse_router_mode(d));
+  if (path != moe::kStream || tb != 16) return false;
+  const int fr = fuse_router_mode(d);
+  if (!is_w4(d->weight_format)) return moe::dma_plan_ok(d->H, d->I, d->T, d->K, d->E, fr);
+  const bool fold = d->weight_format == MOE_WEIGHTS_W4G128_FOLD;
+  const bool wave = moe::wave_w4_shape_ok(d->H, d->I, tb) && (long long)d->T * d->K >= 4LL * d->E && !fold;
+  return !wave && moe::stream_plan_ok(d->H, d->I, d->T, d->K, d->E, fr);
 }
 
 // Shapes the single-workgroup planner does not route itself (T > 32 with
@@ -382,7 +388,10 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
         e = moe::launch_down(xa, L.task_capacity, L.token_block, p->path, p->num_cus, s);
         break;
       case 4: e = moe::launch_combine(xa, s); break;
-      case 5: e = moe::launch_dma_gate_up_planned(xa, ra, p->num_cus, s); break;
+      case 5:
+        e = w4 ? moe::launch_stream_gate_up_planned(xa, ra, L.task_capacity, p->num_cus, s)
+               : moe::launch_dma_gate_up_planned(xa, ra, p->num_cus, s);
+        break;
       default: e = moe::launch_route_plan_multi(ra, s); break;
     }
     if (e != hipSuccess) {

@@ -66,6 +66,10 @@ hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int tok
 hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,
                               int num_cus, hipStream_t s);
 bool stream_shape_ok(int H, int I, bool w4);
+// W4 gate/up that routes and plans in its prologue (no planner launch).
+bool stream_plan_ok(int H, int I, int T, int K, int E, int fuse_router);
+hipError_t launch_stream_gate_up_planned(const ExpertArgs &a, const RouteArgs &ra, int task_capacity,
+                                         int num_cus, hipStream_t s);
 // bf16 streaming GEMMs through LDS (16/32-row tasks), moe_dma.hip.
 bool dma_shape_ok(int H, int I, int token_block);
 hipError_t launch_dma_gate_up(const ExpertArgs &a, int token_block, int num_cus, hipStream_t s);

@@ -184,7 +184,7 @@ constexpr int kSmallPlanWaves = 16;
 struct SmallPlanLds {
   const int *ids;    // [R] expert of route q
   const float *w;    // [R] routing weight of route q
-  int *wcnt;         // [16][E] zeroed before the call; per-wave counts -> prefixes
+  int *wcnt;         // [NT / 64][E] zeroed before the call; per-wave counts -> prefixes
   int *cnt, *off;    // [E]
   int *toff;         // [E + 1]
   int4 *tasks;       // task list
@@ -202,7 +202,9 @@ struct SmallPlanOut {
 // Bits of an expert id below E (E <= 256).
 __device__ __forceinline__ int id_bits(int E) { return E <= 1 ? 1 : 32 - __builtin_clz((unsigned)(E - 1)); }
 
-// Called by all 1024 threads after the routes are visible in LDS.
+// Called by all NT threads of the workgroup (R <= NT routes, one per thread;
+// NT / 64 per-wave count rows in wcnt) after the routes are visible in LDS.
+template <int NT = kSmallPlanRoutes>
 __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go, bool write_global,
                                   int R, int E, int K, int tb, uint32_t flags) {
   const SmallPlanOut *g = write_global ? &go : nullptr;
@@ -286,14 +288,14 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
     g->ranks[q] = -1;
     g->map[q] = -1;
   }
-  for (int p = valid_rows + tid; p < R + 64; p += kSmallPlanRoutes) {
+  for (int p = valid_rows + tid; p < R + 64; p += NT) {
     s.row_token[p] = 0;
     if (g && p < R) {
       g->row_route[p] = -1;
       g->row_token[p] = 0;
     }
   }
-  for (int e = tid; e < E; e += kSmallPlanRoutes) {
+  for (int e = tid; e < E; e += NT) {
     const int c = s.cnt[e];
     int t0 = s.toff[e];
     for (int r0 = 0; r0 < c; r0 += tb, ++t0) {

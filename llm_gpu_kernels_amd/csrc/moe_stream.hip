@@ -33,6 +33,7 @@
 
 #include "common.h"
 #include "moe_internal.h"
+#include "moe_route_dev.h"
 
 #define MOE_CONST __attribute__((address_space(4)))
 
@@ -65,10 +66,26 @@ __device__ __forceinline__ void lds_barrier() {
 // A operand in the folded K order, weights (136 + q) as B, and each group's
 // fp32 sum scaled by the lane's own weight-row scale after subtracting 136 x
 // the group's token sums; effective weights q * scale exactly.
+// PLAN (W4 gate/up, 16-row tasks, router-fused shapes with R <= 512): every
+// workgroup first routes all tokens and plans in LDS (route_dev::route_token
+// and plan_small), workgroup 0 also writes the routing results, the global
+// plan arrays for the down and combine launches and zeroes the work counters
+// (as the planner launch would), and the units' tasks and token rows come
+// from LDS; the separate planner launch is then not needed.
+constexpr int kPlanTasks = route_dev::kMaxExperts + kThreads / 16;  // E + R / 16 bound
+constexpr int kPlanLds = kPlanTasks * 16 + (kThreads + 64) * 4 + 16;
+
 template <int KIND, int MT, int SPW, bool W4, bool FOLD>
-__global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertArgs a) {
+constexpr size_t stream_lds(bool plan) {
+  return (size_t)2 * kWaves * 2 * MT * kWave * sizeof(f32x4) +
+         (FOLD ? (size_t)kWaves * (SPW / 4) * MT * 16 * sizeof(float) : 0) + (plan ? kPlanLds : 0);
+}
+
+template <int KIND, int MT, int SPW, bool W4, bool FOLD, bool PLAN = false>
+__global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertArgs a, RouteArgs ra) {
   constexpr int NRB = 2;
   extern __shared__ f32x4 s_red[];  // [2][kWaves][NRB][MT][64]
+  static_assert(!PLAN || (KIND == 0 && MT == 1 && W4), "planning prologue: 16-row W4 gate/up");
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
@@ -77,7 +94,61 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
   const int H = a.H, I = a.I;
   const int s0 = wave * SPW;
   const int ncb = KIND == 0 ? I / 16 : H / 32;
-  const int total = *as_const(a.num_tasks) * ncb;
+  const int4 *l_tasks = nullptr;
+  const int *l_row = nullptr;
+  int ntasks = 0;
+  if constexpr (PLAN) {
+    using namespace route_dev;
+    uint8_t *pl = (uint8_t *)s_red + stream_lds<KIND, MT, SPW, W4, FOLD>(false);
+    int4 *p_tasks = (int4 *)pl;
+    int *p_row = (int *)(pl + kPlanTasks * 16);
+    int *p_nt = p_row + kThreads + 64;
+    // Scratch in the partial-sum buffers (idle until the first unit's sums).
+    int *x_ids = (int *)s_red;
+    float *x_w = (float *)((uint8_t *)s_red + 4 * kThreads);
+    int *x_wcnt = (int *)((uint8_t *)s_red + 8 * kThreads);
+    int *x_cnt = x_wcnt + kWaves * kMaxExperts;
+    int *x_off = x_cnt + kMaxExperts;
+    int *x_toff = x_off + kMaxExperts;
+    uint32_t *x_flags = (uint32_t *)(x_toff + kMaxExperts + 1);
+    // One token per wave (fuse_router 1, T <= 16) or half-wave (2, T <= 32):
+    // two rounds of the eight waves; every round's logits are requested first.
+    const bool half = ra.fuse_router == 2;
+    const int per_round = half ? 2 * kWaves : kWaves;
+    float raw[2][4];
+    int ft[2];
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      ft[rd] = rd * per_round + (half ? 2 * wave + (lane >> 5) : wave);
+      if (half) load_token_logits<true>(ra.logits, ft[rd], ft[rd] < ra.T, ra.E, raw[rd]);
+      else load_token_logits<false>(ra.logits, ft[rd], ft[rd] < ra.T, ra.E, raw[rd]);
+    }
+    for (int i = tid; i < kWaves * ra.E; i += kThreads) x_wcnt[i] = 0;
+    if (tid == 0) *x_flags = 0;
+    const bool g0 = blockIdx.x == 0;
+    if (g0 && tid < 4) ra.counters[tid] = 0;
+    uint32_t flags = 0;
+    int32_t *ids_g = g0 ? (int32_t *)ra.ids : nullptr;
+    float *w_g = g0 ? ra.weights : nullptr;
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const bool fwave = rd * per_round + (half ? 2 * wave : wave) < ra.T;  // wave-uniform
+      if (!fwave) continue;
+      if (half)
+        route_token<true>(raw[rd], ft[rd], ft[rd] < ra.T, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+      else
+        route_token<false>(raw[rd], ft[rd], true, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+    }
+    __syncthreads();
+    const SmallPlanLds L{x_ids, x_w, x_wcnt, x_cnt, x_off, x_toff, p_tasks, p_row, p_nt, x_flags};
+    const SmallPlanOut O{ra.counts, ra.offsets, ra.ranks, ra.map, ra.row_route, ra.row_token,
+                         ra.tasks, ra.num_tasks, ra.status};
+    plan_small<kThreads>(L, O, g0, ra.R, ra.E, ra.K, 16, flags);
+    ntasks = *p_nt;
+    l_tasks = p_tasks;
+    l_row = p_row;
+  }
+  const int total = (PLAN ? ntasks : *as_const(a.num_tasks)) * ncb;
   // Each workgroup takes a block of consecutive units, i.e. mostly one
   // task, so the token rows (B) stay in registers from unit to unit and are
   // reloaded only when the task changes (round-robin units, B reloaded per
@@ -105,10 +176,18 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
     const int t = u / ncb;
     m.task = t;
     m.cb = u - t * ncb;
-    m.expert = tasks[4 * t];
-    m.row0 = tasks[4 * t + 1];
-    m.rows = tasks[4 * t + 2];
-    m.idxv = row_vec[m.row0 + (lane & 31)];
+    if constexpr (PLAN) {
+      const int4 tk = l_tasks[t];
+      m.expert = __builtin_amdgcn_readfirstlane(tk.x);
+      m.row0 = __builtin_amdgcn_readfirstlane(tk.y);
+      m.rows = __builtin_amdgcn_readfirstlane(tk.z);
+      m.idxv = l_row[m.row0 + (lane & 31)];
+    } else {
+      m.expert = tasks[4 * t];
+      m.row0 = tasks[4 * t + 1];
+      m.rows = tasks[4 * t + 2];
+      m.idxv = row_vec[m.row0 + (lane & 31)];
+    }
     return m;
   };
 
@@ -369,11 +448,11 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
   }
 }
 
-template <int KIND, int MT, int SPW, bool W4, bool FOLD = false>
-hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s) {
-  auto k = stream_kernel<KIND, MT, SPW, W4, FOLD>;
-  const size_t lds = (size_t)2 * kWaves * 2 * MT * kWave * sizeof(f32x4) +
-                     (FOLD ? (size_t)kWaves * (SPW / 4) * MT * 16 * sizeof(float) : 0);
+template <int KIND, int MT, int SPW, bool W4, bool FOLD = false, bool PLAN = false>
+hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStream_t s,
+                      const RouteArgs *ra = nullptr) {
+  auto k = stream_kernel<KIND, MT, SPW, W4, FOLD, PLAN>;
+  const size_t lds = stream_lds<KIND, MT, SPW, W4, FOLD>(PLAN);
   static int per_cu = [&] {
     int n = 1;
     (void)hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -389,7 +468,8 @@ hipError_t launch_one(const ExpertArgs &a, int units_bound, int num_cus, hipStre
   int grid = num_cus * per_cu;
   if (grid > units_bound) grid = units_bound;
   if (grid < 1) grid = 1;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, s, a);
+  RouteArgs none{};
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, s, a, ra ? *ra : none);
   return hipGetLastError();
 }
 
@@ -441,6 +521,19 @@ hipError_t launch_stream_gate_up(const ExpertArgs &a, int task_capacity, int tok
               : launch_spw<0, 1, false>(a, spw, units, num_cus, s);
   return w4 ? launch_spw<0, 2, true>(a, spw, units, num_cus, s)
             : launch_spw<0, 2, false>(a, spw, units, num_cus, s);
+}
+
+bool stream_plan_ok(int H, int I, int T, int K, int E, int fuse_router) {
+  return stream_shape_ok(H, I, true) && H / 256 == 8 && fuse_router != 0 && T * K <= kThreads &&
+         E <= route_dev::kMaxExperts && T <= 32;
+}
+
+hipError_t launch_stream_gate_up_planned(const ExpertArgs &a, const RouteArgs &ra, int task_capacity,
+                                         int num_cus, hipStream_t s) {
+  const int units = task_capacity * (a.I / 16);
+  if (a.H != 2048) return hipErrorInvalidValue;
+  if (a.w4_fold) return launch_one<0, 1, 8, true, true, true>(a, units, num_cus, s, &ra);
+  return launch_one<0, 1, 8, true, false, true>(a, units, num_cus, s, &ra);
 }
 
 hipError_t launch_stream_down(const ExpertArgs &a, int task_capacity, int token_block,

@@ -87,7 +87,7 @@ def test_layout_for_qwen_shape():
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=32))
     assert lay.launches == 3
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, fmt=N.WEIGHTS_W4G128))
-    assert lay.launches == 4  # W4: router fused into the planner
+    assert lay.launches == 3  # W4: routing and planning in the gate/up launch too
     rc2, lay2 = _layout(_desc(route=N.ROUTE_LOGITS, T=17, fmt=N.WEIGHTS_W4G128_FOLD))
     assert rc2 == 0 and (lay2.total, lay2.launches, lay2.fast_path) == (lay.total, lay.launches, lay.fast_path)
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=17, H=4096))

@@ -33,10 +33,10 @@ FAMILIES = [
     ("bf16-t193-planner-dma", 193, "uniform", False, 4),      # multi-workgroup planner + counter-scheduled dma
     ("bf16-t384-32row-dma", 384, "uniform", False, 4),        # 32-row tasks, 32-row down units in fours
     ("bf16-t1024-zipf-tiled", 1024, "zipf", False, 4),        # LDS-tiled GEMMs, 64-row tasks
-    ("w4-t17-stream", 17, "uniform", True, 4),                # W4 register-streaming gate/up
+    ("w4-t17-stream", 17, "uniform", True, 3),                # W4 register-streaming gate/up, routing prologue
     ("w4-t193-wave", 193, "uniform", True, 4),                # W4 one-unit-per-wave gate/up
     ("w4-t1024-wave", 1024, "uniform", True, 4),              # W4 wave gate/up, 64-row tasks
-    ("w4fold-t17-stream", 17, "uniform", "fold", 4),          # folded decode, split-K streaming
+    ("w4fold-t17-stream", 17, "uniform", "fold", 3),          # folded decode, split-K streaming, routing prologue
     ("w4fold-t193-stream", 193, "uniform", "fold", 4),        # folded decode, 16-row tasks
 ]
 

@@ -558,6 +558,39 @@ def test_gate_up_with_planning_prologue(tokens, gpu_device):
     assert plan.read_status() & 4
 
 
+@pytest.mark.parametrize("tokens,decode", [(1, "exact"), (16, "exact"), (17, "exact"), (32, "exact"),
+                                           (16, "fold"), (17, "fold"), (31, "fold")])
+def test_w4_gate_up_with_planning_prologue(tokens, decode, gpu_device):
+    """W4 Qwen shape, T <= 32: the register-streaming W4 gate/up routes and
+    plans in its prologue (one token per wave in two rounds up to T = 16, two
+    per wave above), so the forward is three launches.  IDs bit-exact on
+    tie-heavy logits, every global plan array equal to the canonical dispatch,
+    the work counters zero, the layer within tolerance, and bitwise equal to
+    the fixed-route W4 path (planner launch) on the same routes."""
+    lay = make_layer("qwen", tokens, seed=40 + tokens, device=gpu_device)
+    packed = quantize_gate_up(lay["gate_up"].cpu())
+    tiled = tile_gate_up(packed).to(gpu_device)
+    g = torch.Generator().manual_seed(tokens + 1)
+    logits = (torch.randint(-6, 6, (tokens, lay["E"]), generator=g).float() * 0.75).to(gpu_device)
+    plan = prepare_routed_moe(lay["x"], logits, tiled, lay["down"], 8, w4_decode=decode)
+    assert plan.launch_names == ("gate_up_swiglu", "down", "combine")
+    out = plan.forward().clone()
+    torch.cuda.synchronize()
+    ids, w = O.route_topk(logits.cpu(), 8)
+    assert torch.equal(plan.ids.cpu(), ids), "router IDs differ"
+    assert torch.allclose(plan.routing_weights.cpu(), w, rtol=2e-6, atol=1e-7)
+    _check_dispatch(plan, ids, lay["E"])
+    assert plan.read_status() == 0
+    assert plan.work_counters.cpu().tolist() == [0, 0, 0, 0]
+    deq = (O.dequantize_w4_unrounded if decode == "fold" else O.dequantize_w4)(packed.words, packed.scales)
+    m = O.error(out, O.moe_reference(lay["x"].cpu(), deq, lay["down"].cpu(), ids, w))
+    assert m["passed"], m
+    fixed = prepare_w4_moe(lay["x"], tiled, lay["down"], plan.ids.clone(), plan.routing_weights.clone(),
+                           w4_decode=decode)
+    assert len(fixed.launches) == 4
+    assert torch.equal(fixed.run().view(torch.int16), out.view(torch.int16))
+
+
 QWEN_PERF = [c for c in GOLDEN["cases"] if c["family"] == "performance_cases" and c["E"] == 128]
 
 
