@@ -41,12 +41,19 @@ extern "C" {
 #define MOE_STATUS_BAD_ID 1u      /* an expert ID outside [0, E)              */
 #define MOE_STATUS_BAD_WEIGHT 2u  /* a non-finite routing weight              */
 #define MOE_STATUS_BAD_LOGIT 4u   /* a non-finite router logit (router mode)  */
-#define MOE_STATUS_STALLED 16u    /* a bounded cross-workgroup wait of the planner
-                                     ran out (never expected; results invalid)   */
-#define MOE_STATUS_DIRTY_COUNTERS 8u /* read_status only: the work counters were
-                                        not zero after the stream drained (a launch
-                                        that did not complete, or a workspace that
-                                        was not zeroed); moe_plan_reset_counters or
+#define MOE_STATUS_STALLED 16u    /* the multi-workgroup planner's view was
+                                     incomplete: a bounded cross-workgroup wait ran
+                                     out (its workgroups did not all become resident
+                                     together, e.g. another stream's kernel held CUs)
+                                     or a published count failed its bounds (a
+                                     workspace that was not zeroed).  The forward
+                                     then ran no GEMM tasks: the output is invalid */
+#define MOE_STATUS_DIRTY_COUNTERS 8u /* the work counters were not zero when a
+                                        counter-scheduled GEMM launched (the launch
+                                        counts the units it ran and latches this bit
+                                        when the count is off: the output is invalid),
+                                        or read_status found them nonzero after the
+                                        stream drained.  moe_plan_reset_counters or
                                         any later complete forward clears them     */
 
 /* moe_desc.weight_format */
@@ -131,12 +138,17 @@ const char *moe_last_error(void);
 int moe_workspace_layout(const moe_desc *d, moe_layout *out);
 
 /* Validate the descriptor and bind its pointers.  No allocation, no launch,
- * no device work (so it may run during stream capture).  The workspace should
- * be zeroed once before its first forward: the streaming GEMMs hand out work
- * from four counters that must read zero when they start.  Every complete
- * forward leaves them at zero, and the planner and combine launches zero
- * them as well, so a dirty workspace heals after one forward; use
- * moe_plan_reset_counters to clean one before its first forward. */
+ * no device work (so it may run during stream capture).  The workspace must
+ * be zeroed before its first forward (or cleaned with moe_plan_reset_counters):
+ * the streaming GEMMs hand out work from four counters that must read zero
+ * when they start, and the multi-workgroup planner takes only words tagged
+ * with the current launch's epoch from its exchange area, which a zeroed area
+ * never holds.  Every complete forward leaves both clean.  A forward that
+ * finds them dirty reports MOE_STATUS_DIRTY_COUNTERS or MOE_STATUS_STALLED
+ * and the next forward is clean again.  The multi-workgroup planner (fixed
+ * routes, or T > 32 with logits) assumes its workgroups (at most one per CU)
+ * become resident together: a kernel of another stream that holds CUs for
+ * its whole duration makes it report MOE_STATUS_STALLED instead of hanging. */
 int moe_plan_create(moe_plan **out, const moe_desc *d);
 /* Enqueue one forward on `stream` (hipStream_t; NULL = default stream).
  * No host sync and no allocation; T == 0 launches nothing. */

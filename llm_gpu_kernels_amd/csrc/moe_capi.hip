@@ -14,6 +14,7 @@
 
 #include "../../include/moe_mi355x.h"
 #include "moe_internal.h"
+#include <stdlib.h>
 
 namespace {
 
@@ -159,7 +160,7 @@ moe_layout compute_layout(const moe_desc *d) {
   {
     const int tpw = moe::multi_plan_tokens(d->K, d->route_mode == MOE_ROUTE_LOGITS);
     const size_t W = tpw > 0 ? ((size_t)d->T + tpw - 1) / tpw : 0;
-    L.partials = take(W * ((size_t)d->E + 1) * 4);
+    L.partials = take(W * ((size_t)d->E + 1) * 4 + 4);  // + the planner's arrival counter
   }
   L.act = take(R * (size_t)d->I * 2);
   L.routed = take(R * (size_t)d->H * 2);
@@ -191,6 +192,7 @@ struct moe_plan {
   int fuse_router;  // 0: router launch, 1: one token per planner wave, 2: two
   bool planned;     // gate/up routes and plans in its prologue (no planner launch)
   bool multi;       // multi-workgroup router + planner launch
+  bool test_planner_hold;  // MOE_TEST_PLANNER_HOLD=1 at create: see run_stages
   int path;
 };
 
@@ -238,6 +240,10 @@ int bind_plan(moe_plan *p, const moe_desc *d) {
     e = hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
   if (e != hipSuccess) return hip_fail(e, "device query");
   p->multi = multi_planner(d, path, L.token_block, p->num_cus);
+  {
+    const char *h = getenv("MOE_TEST_PLANNER_HOLD");
+    p->test_planner_hold = h && h[0] == '1';
+  }
   p->L.launches = launch_count(d, path, L.token_block, p->num_cus);
   return MOE_OK;
 }
@@ -341,6 +347,15 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   ra.token_block = L.token_block;
   ra.partials = (int32_t *)(ws + L.partials);
   ra.plan_tpw = moe::multi_plan_tokens(d.K, ra.route_logits);
+  ra.plan_spin_cap = moe::kMultiSpinCap;
+  ra.plan_hold_wg = -1;
+  // Test hook (failure-handling tests only): the last planner workgroup
+  // withholds its counts and every wait gives up after a few rounds, so the
+  // stalled-plan path runs with every kernel exiting normally.
+  if (p->test_planner_hold) {
+    ra.plan_spin_cap = 64;
+    ra.plan_hold_wg = (d.T + ra.plan_tpw - 1) / ra.plan_tpw - 1;
+  }
 
   moe::ExpertArgs xa;
   xa.x = (const uint16_t *)d.x;
@@ -357,6 +372,7 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   xa.offsets = ra.offsets;
   xa.tasks = ra.tasks;
   xa.counters = ra.counters;
+  xa.status = ra.status;
   xa.act = (uint16_t *)(ws + L.act);
   xa.routed = (uint16_t *)(ws + L.routed);
   xa.out = (uint16_t *)d.out;

@@ -95,8 +95,17 @@ constexpr int kSeqRing = 8;
 template <int KIND, int MT>
 constexpr int kChunkOf = KIND == 1 && MT == 2 ? 4 : 2;
 
-__device__ __forceinline__ void finish_units(int32_t *w, int G) {
-  if (atomicAdd(w + 1, 1) == G - 1) {
+// The finishing add also carries the workgroup's unit count (bits 12 and
+// up; grids stay below 4096 workgroups), so the last workgroup knows how many
+// units the launch ran.  Anything but exactly `total` means the counters were
+// not zero at launch (a workspace that was not zeroed, a launch that did not
+// complete): units were skipped or run twice, and the launch latches
+// MOE_STATUS_DIRTY_COUNTERS into status[0] instead of returning a wrong
+// result with a clean status.
+__device__ __forceinline__ void finish_units(int32_t *w, int G, int units, int total, uint32_t *status) {
+  const uint32_t old = (uint32_t)atomicAdd(w + 1, 1 + (units << 12));
+  if ((old & 0xfffu) == (uint32_t)G - 1u) {
+    if ((int)(old >> 12) + units != total) atomicOr(status, kStatusDirtyCounters);
     atomicExch(w, 0);
     atomicExch(w + 1, 0);
   }
@@ -226,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   constexpr int S = A;
   const int ub = (int)blockIdx.x * S;  // this workgroup's first unit
   if (ub >= total) {
-    if (tid == 0) finish_units(wcnt, G);
+    if (tid == 0) finish_units(wcnt, G, 0, total, a.status);
     return;
   }
   const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
@@ -421,6 +430,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   auto unit_at = [&](int k) -> int { return k < S ? ub + k : seq[k % kSeqRing]; };
   Meta prev, cur = meta_of(ub), next;
   load_b(cur, bfr);
+  int done_units = 0;  // units this workgroup ran (known when its loop ends)
   int taken = 0;       // wave 0, lane 0: counter value of the unit taken last
   bool taking = true;  // wave 0: the units taken so far are all in range
   bool pending = false;
@@ -497,6 +507,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     if (un >= total) {
       lds_barrier();
       epilogue(prev, i % C::PAR, i & 1);
+      done_units = i + 1;
       break;
     }
     if (next.task != cur.task) {
@@ -515,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   // here) before it counts itself finished.
   if (wave == 0) {
     __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
-    if (lane == 0) finish_units(wcnt, G);
+    if (lane == 0) finish_units(wcnt, G, done_units, total, a.status);
   }
 }
 
@@ -529,6 +540,7 @@ hipError_t launch_one(const ExpertArgs &a, int num_cus, hipStream_t s, const Rou
                                                (int)lds) == hipSuccess;
   if (!attr) return hipErrorInvalidValue;
   RouteArgs none{};
+  if (num_cus >= 4096) return hipErrorInvalidValue;  // finish_units packs the grid size in 12 bits
   hipLaunchKernelGGL(k, dim3(num_cus > 0 ? num_cus : 1), dim3(kThreads), lds, s, a, ra ? *ra : none);
   return hipGetLastError();
 }

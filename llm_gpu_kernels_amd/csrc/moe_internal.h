@@ -22,10 +22,16 @@ struct RouteArgs {
   int route_logits, renormalize, id64, fuse_router;
   int token_block;
   int plan_tpw;            // multi-workgroup planner: tokens per workgroup
+  int plan_spin_cap;       // multi-workgroup planner: re-reads of a batch before it gives up
+  int plan_hold_wg;        // test hook: this workgroup never publishes (-1: none)
 };
+
+// Multi-workgroup planner wait bound (re-read rounds of about 1 us).
+constexpr int kMultiSpinCap = 1 << 20;
 
 // Status bit set when a bounded cross-workgroup wait ran out (never expected).
 constexpr uint32_t kStatusStalled = 16u;
+constexpr uint32_t kStatusDirtyCounters = 8u;
 
 // Expert stage: gate/up + SwiGLU, down projection, weighted combine.
 struct ExpertArgs {
@@ -39,6 +45,7 @@ struct ExpertArgs {
   const int32_t *counts, *offsets;  // [E] rows per expert and their first grouped row
   const int4 *tasks;
   int32_t *counters;           // [4] {units taken, workgroups done} of gate/up, down
+  uint32_t *status;            // [4] status words (status[0]: MOE_STATUS_* bits)
   uint16_t *act;               // [R, I] bf16, grouped-row order
   uint16_t *routed;            // [R, H] bf16, route order
   uint16_t *out;               // [T, H] bf16

@@ -332,7 +332,6 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(RouteArgs a) {
 // exceeds its spin bound sets status bit MOE_STATUS_STALLED instead of hanging.
 constexpr int kMultiThreads = 1024;
 constexpr int kMultiWaves = kMultiThreads / kWave;
-constexpr int kMultiSpinCap = 1 << 20;
 constexpr int kMultiBatch = 16;  // published words read per thread per round trip
 
 __device__ __forceinline__ uint32_t coherent_load(const uint32_t *p) {
@@ -429,9 +428,9 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
       run += c;
     }
     // 3. publish the chunk's count of expert e.
-    coherent_store(part + (size_t)w * (E + 1) + e, (tag << 16) | (uint32_t)run);
+    if (w != a.plan_hold_wg) coherent_store(part + (size_t)w * (E + 1) + e, (tag << 16) | (uint32_t)run);
   }
-  if (tid == 0) coherent_store(part + (size_t)w * (E + 1) + E, (tag << 16) | s_flags);
+  if (tid == 0 && w != a.plan_hold_wg) coherent_store(part + (size_t)w * (E + 1) + E, (tag << 16) | s_flags);
   __syncthreads();
   if (ok) s_lrank[tid] = s_wcnt[wave][id] + lrank;
 
@@ -464,7 +463,7 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
 #pragma unroll
         for (int i = 0; i < kMultiBatch; ++i) all &= (v[i] >> 16) == tag;
         if (all) break;
-        if (n >= kMultiSpinCap) {
+        if (n >= a.plan_spin_cap) {
           stalled = true;
           break;
         }
@@ -476,8 +475,15 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
         if (j >= nwords) continue;
         const uint32_t c = v[i] & 0xffffu;
         const int src = j / (E + 1), e = j - src * (E + 1);
+        // A word that cannot have been published by workgroup src (a count
+        // above its route count, unknown flag bits) marks the plan invalid,
+        // so no index is ever formed from it.
+        const int src_routes = (min(a.T, (src + 1) * tpw) - src * tpw) * K;
         if (e == E) {
-          fl |= c;
+          if (c & ~7u) stalled = true;
+          fl |= c & 7u;
+        } else if ((int)c > src_routes) {
+          stalled = true;
         } else if (c) {
           atomicAdd(&s_tot[e], (int)c);
           if (src < w) atomicAdd(&s_base[e], (int)c);
@@ -514,55 +520,71 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
       crun += c[j];
       trun += nt[j];
     }
-    if (lane == kWave - 1) s_toff[E] = trun;
+    if (lane == kWave - 1) {
+      s_toff[E] = trun;
+      // Totals above R (possible only from words that were never published
+      // in this launch) would place rows past the arrays.
+      if (crun > a.R) atomicOr(&s_all_flags, kStatusStalled);
+    }
   }
   __syncthreads();
 
   // 5. this chunk's rows; workgroup 0 the expert-level arrays.  A workgroup
-  // whose wait ran out writes only the status bit (its counts may be
-  // garbage); if it is workgroup 0 the forward has no tasks.
-  if (s_all_flags & kStatusStalled) {
-    if (tid == 0) {
-      atomicOr(a.status, kStatusStalled);
-      if (w == 0) *a.num_tasks = 0;
+  // whose view is incomplete (a wait ran out, or a word failed its bounds)
+  // writes nothing.  Every workgroup then arrives on one counter, carrying
+  // whether its view was complete; the last to arrive is the only writer of
+  // status[0], num_tasks and the epoch: the task count when every view was
+  // complete, else no tasks and MOE_STATUS_STALLED, so the GEMMs never read
+  // rows a workgroup did not write.  It runs after every workgroup of the
+  // launch has read the epoch (each reads it before it arrives), so no
+  // workgroup of this launch can see the advanced value, and words left by
+  // this launch never carry the next launch's tag.
+  const uint32_t all_flags = s_all_flags;
+  const bool bad = (all_flags & kStatusStalled) != 0;
+  uint32_t *const arrive = part + (size_t)W * (E + 1);
+  uint32_t before = 0;
+  if (tid == 0)
+    before = __hip_atomic_fetch_add(arrive, 1u + (bad ? 1u << 16 : 0u), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  if (!bad) {
+    if (valid) {
+      const int q = q0 + tid;
+      if (ok) {
+        const int rank = s_base[id] + s_lrank[tid];
+        const int p = s_off[id] + rank;
+        a.ranks[q] = rank;
+        a.map[q] = p;
+        a.row_route[p] = q;
+        a.row_token[p] = q / K;
+      } else {
+        a.ranks[q] = -1;
+        a.map[q] = -1;
+      }
     }
-    return;
+    if (w == 0) {
+      const int valid_rows = s_off[E - 1] + s_tot[E - 1];
+      for (int p = valid_rows + tid; p < a.R; p += kMultiThreads) {
+        a.row_route[p] = -1;
+        a.row_token[p] = 0;
+      }
+      const int tb = a.token_block;
+      for (int e = tid; e < E; e += kMultiThreads) {
+        const int c = s_tot[e];
+        int tt = s_toff[e];
+        for (int r0 = 0; r0 < c; r0 += tb, ++tt) a.tasks[tt] = make_int4(e, s_off[e] + r0, min(tb, c - r0), 0);
+      }
+      if (tid == 0) a.counters[0] = a.counters[1] = a.counters[2] = a.counters[3] = 0;
+    }
   }
-  if (valid) {
-    const int q = q0 + tid;
-    if (ok) {
-      const int rank = s_base[id] + s_lrank[tid];
-      const int p = s_off[id] + rank;
-      a.ranks[q] = rank;
-      a.map[q] = p;
-      a.row_route[p] = q;
-      a.row_token[p] = q / K;
-    } else {
-      a.ranks[q] = -1;
-      a.map[q] = -1;
-    }
-  }
-  if (w == 0) {
-    const int valid_rows = s_off[E - 1] + s_tot[E - 1];
-    for (int p = valid_rows + tid; p < a.R; p += kMultiThreads) {
-      a.row_route[p] = -1;
-      a.row_token[p] = 0;
-    }
-    const int tb = a.token_block;
-    for (int e = tid; e < E; e += kMultiThreads) {
-      const int c = s_tot[e];
-      int tt = s_toff[e];
-      for (int r0 = 0; r0 < c; r0 += tb, ++tt) a.tasks[tt] = make_int4(e, s_off[e] + r0, min(tb, c - r0), 0);
-    }
-    if (tid == 0) {
-      *a.num_tasks = s_toff[E];
-      a.status[0] = s_all_flags;
-      a.status[1] = 0;
-      a.counters[0] = a.counters[1] = a.counters[2] = a.counters[3] = 0;
-      // Every workgroup read the epoch before publishing, and every
-      // publication has been seen: the next launch may use the next tag.
-      coherent_store(a.status + 2, coherent_load(a.status + 2) + 1u);
-    }
+  if (tid == 0 && (before & 0xffffu) == (uint32_t)W - 1u) {
+    const bool any_bad = bad || (before >> 16) != 0;
+    // status[1]: bits of a separate router launch earlier on this stream.
+    uint32_t st = a.status[1] | (any_bad ? (all_flags & 7u) | kStatusStalled : all_flags);
+    a.status[0] = st;
+    a.status[1] = 0;
+    *a.num_tasks = any_bad ? 0 : s_toff[E];
+    coherent_store(arrive, 0u);
+    coherent_store(a.status + 2, coherent_load(a.status + 2) + 1u);
   }
 }
 

@@ -308,7 +308,9 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
   __syncthreads();
   if (g && tid == 0) {
     *g->num_tasks = s.toff[E];
-    g->status[0] = *s.flags;
+    // Write-through: a later workgroup of the same launch may OR a bit into
+    // this word from another XCD (the work-accounting check of the GEMMs).
+    __hip_atomic_store(g->status, *s.flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

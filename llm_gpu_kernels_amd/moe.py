@@ -270,9 +270,14 @@ class PreparedMoE:
     def check_inputs(self):
         """Synchronising debug check of the last forward (moe.py:157-160)."""
         flags = self.read_status()
+        if flags & N.STATUS_STALLED:
+            raise RuntimeError(f"MoE planner did not complete (GPU status={flags}): its "
+                               "workgroups were not resident together or its exchange area "
+                               "was not zeroed; the forward ran no expert tasks")
         if flags & N.STATUS_DIRTY_COUNTERS:
-            raise RuntimeError(f"MoE workspace work counters are not zero (GPU status={flags}): "
-                               "a launch did not complete; call reset_counters()")
+            raise RuntimeError(f"MoE workspace work counters were not zero (GPU status={flags}): "
+                               "a launch did not complete or the workspace was not zeroed; "
+                               "the last output is invalid (call reset_counters())")
         if flags:
             raise ValueError(f"invalid runtime MoE inputs: GPU status={flags} "
                              "(1=IDs, 2=nonfinite weights, 4=nonfinite logits)")
@@ -368,6 +373,19 @@ class PreparedRoutedMoE(PreparedMoE):
     """
 
     def forward(self, hidden=None, router_logits=None):
+        # Same rules as prepare_routed_moe: a bound buffer is only ever
+        # overwritten by a tensor of its own shape, dtype and device (no
+        # broadcast of a [1, H] row, no silent fp32 -> bf16 cast).
+        for name, new, bound in (("hidden", hidden, self.x), ("router_logits", router_logits, self.logits)):
+            if new is None:
+                continue
+            if not isinstance(new, torch.Tensor):
+                raise ValueError(f"{name} must be a tensor")
+            if tuple(new.shape) != tuple(bound.shape) or new.dtype != bound.dtype:
+                raise ValueError(f"{name} must be {bound.dtype} {list(bound.shape)}, got "
+                                 f"{new.dtype} {list(new.shape)}")
+            if new.device != bound.device:
+                raise ValueError(f"{name} must be on {bound.device}, got {new.device}")
         if hidden is not None and hidden.data_ptr() != self.x.data_ptr():
             self.x.copy_(hidden)
         if router_logits is not None and router_logits.data_ptr() != self.logits.data_ptr():

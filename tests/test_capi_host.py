@@ -228,7 +228,7 @@ def test_attention_out_storage_check():
 def test_status_bit_values():
     """Status bits of the header, as the Python layer reads them."""
     text = (INCLUDE / "moe_mi355x.h").read_text()
-    for name, value in (("BAD_ID", 1), ("BAD_WEIGHT", 2), ("BAD_LOGIT", 4), ("DIRTY_COUNTERS", 8)):
+    for name, value in (("BAD_ID", 1), ("BAD_WEIGHT", 2), ("BAD_LOGIT", 4), ("DIRTY_COUNTERS", 8), ("STALLED", 16)):
         assert re.search(rf"#define MOE_STATUS_{name} {value}u", text), name
         assert getattr(N, f"STATUS_{name}") == value
 

@@ -177,9 +177,71 @@ def test_dirty_counters_are_reported_and_healed(gpu_device):
     torch.cuda.synchronize(gpu_device)
     p17.work_counters.copy_(torch.tensor([3, 1, 3, 1], dtype=torch.int32))
     p17.run()
+    torch.cuda.synchronize(gpu_device)
+    # The dirty forward's units counter started at 3: the gate/up launch ran
+    # fewer units than it has and latches bit 8 instead of a clean status.
+    assert p17.read_status() & 8
+    with pytest.raises(RuntimeError, match="work counters"):
+        p17.check_inputs()
     assert torch.equal(_bits(p17.run()), ref)
     torch.cuda.synchronize(gpu_device)
     assert p17.read_status() == 0
     p17.work_counters.copy_(torch.tensor([3, 1, 3, 1], dtype=torch.int32))
     p17.reset_counters()
     assert torch.equal(_bits(p17.run()), ref)
+
+
+def _planner_words(plan):
+    """The multi-workgroup planner's exchange area: [W][E+1] tagged words and
+    its arrival counter (int32 view of the workspace)."""
+    lay = plan.layout
+    return plan.workspace[lay.partials:lay.act].view(torch.int32)
+
+
+@pytest.mark.parametrize("garbage", [False, True], ids=["withheld", "withheld-garbage"])
+def test_stalled_planner_runs_no_tasks(garbage, gpu_device, monkeypatch):
+    """A planner workgroup whose counts never arrive (forced from the host:
+    the test hook makes the last workgroup withhold its words and every wait
+    give up after a few rounds, so every kernel exits normally) leaves an
+    incomplete view: the forward reports MOE_STATUS_STALLED, runs no GEMM
+    task, advances the epoch and leaves the arrival counter at zero.  With
+    garbage carrying the current epoch's tag in the withheld slot, every
+    workgroup rejects the impossible counts the same way.  A plan created
+    without the hook on the same shape is correct."""
+    gate_up, ref_gu, down = _weights(False, gpu_device)
+    lay = make_layer("qwen", 193, seed=11, device=gpu_device, weights=False)
+    ids, w = O.route_topk(lay["logits"].cpu(), 8)
+    ids_d, w_d = ids.to(gpu_device), w.to(gpu_device)
+    monkeypatch.setenv("MOE_TEST_PLANNER_HOLD", "1")
+    plan = prepare_moe(lay["x"], gate_up, down, ids_d, w_d)  # runs one forward
+    monkeypatch.delenv("MOE_TEST_PLANNER_HOLD")
+    torch.cuda.synchronize(gpu_device)
+    assert plan.read_status() & 16
+    with pytest.raises(RuntimeError, match="planner"):
+        plan.check_inputs()
+    words = _planner_words(plan)
+    e = 128
+    tpw = 1024 // 8  # fixed routes: 1024 / K tokens per planner workgroup
+    W = (193 + tpw - 1) // tpw
+    if garbage:
+        st = plan.workspace[plan.layout.status:plan.layout.status + 16].view(torch.int32).cpu()
+        tag = (int(st[2]) & 0x7FFF) | 0x8000
+        junk = torch.full(((e + 1),), (tag << 16) | 0xFFFF, dtype=torch.int64)
+        junk = torch.where(junk >= 2**31, junk - 2**32, junk).to(torch.int32)
+        words[(W - 1) * (e + 1):W * (e + 1)].copy_(junk.to(gpu_device))
+    st0 = int(plan.workspace[plan.layout.status:plan.layout.status + 16].view(torch.int32)[2])
+    plan.run()
+    torch.cuda.synchronize(gpu_device)
+    st = plan.workspace[plan.layout.status:plan.layout.status + 16].view(torch.int32).cpu()
+    assert int(st[0]) & 16
+    assert int(st[2]) == st0 + 1, "the epoch advances on a stalled launch too"
+    assert int(plan.num_tasks.item()) == 0
+    assert int(words[W * (e + 1)].item()) == 0, "arrival counter back at zero"
+    assert int(plan.work_counters.abs().sum().item()) == 0
+    # Without the hook: a new plan on this shape is correct and clean.
+    good = prepare_moe(lay["x"], gate_up, down, ids_d, w_d)
+    out = good.run()
+    torch.cuda.synchronize(gpu_device)
+    assert good.read_status() == 0
+    m = O.error(out, O.moe_reference(lay["x"].cpu(), ref_gu, down.cpu(), ids, w))
+    assert m["passed"], m

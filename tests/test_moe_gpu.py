@@ -714,3 +714,23 @@ def test_multi_workgroup_router(gpu_device):
     plan.logits[tokens - 3, 17] = float("nan")
     plan.forward()
     assert plan.read_status() & 4
+
+
+def test_forward_rejects_mismatched_inputs(gpu_device):
+    """forward(hidden, router_logits) copies only tensors of the bound shape,
+    dtype and device (the prepare-time rules, moe.py:220-235): no broadcast of
+    a [1, H] row, no silent fp32 cast, no host tensors."""
+    lay = make_layer("tiny", 17, seed=3, device=gpu_device)
+    plan = prepare_routed_moe(lay["x"], lay["logits"], lay["gate_up"], lay["down"], lay["K"])
+    ref = plan.forward(lay["x"].clone(), lay["logits"].clone()).clone()
+    bad = [
+        (lay["x"][:1].clone(), None),                        # [1, H] would broadcast
+        (lay["x"].float(), None),                            # fp32 hidden
+        (lay["x"].cpu(), None),                              # host tensor
+        (None, lay["logits"][:, :4].clone()),                # wrong E
+        (None, lay["logits"].double()),                      # fp64 logits
+    ]
+    for hidden, logits in bad:
+        with pytest.raises(ValueError):
+            plan.forward(hidden, logits)
+    assert torch.equal(plan.forward(lay["x"].clone(), lay["logits"].clone()), ref)
