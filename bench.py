@@ -6,7 +6,8 @@ A step is one full router-inclusive MoE layer forward (router -> planner ->
 gate/up+SwiGLU -> down -> combine) over inputs already resident in HBM,
 replayed from HIP graphs of 8 forwards each (BASELINE's timing protocol).  Two
 copies of the weights alternate between forwards so the 256 MB Infinity Cache
-cannot serve a forward from the previous one.  The
+cannot serve a forward from the previous one (more copies where one is small,
+up to 8; a workload that still fits is marked ``cache_resident``).  The
 JSON line's ``value`` is tokens/s of ``--workload`` (default: BASELINE
 configs[1], Qwen3-30B-A3B shape, BF16, T=17); ``sweep`` carries every
 BASELINE MoE configuration.  ``roofline`` is the dominant kernel
@@ -54,14 +55,33 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_plans(spec, device, copies=2):
-    """Prepared layers sharing inputs, each with its own weight copy."""
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+MAX_COPIES = FORWARDS_PER_GRAPH = 8
+
+
+def weight_bytes(spec, lay):
+    """Bytes of one copy of the layer's expert weights (all experts)."""
+    e, h, inter = lay["E"], lay["H"], lay["I"]
+    gu = 2 * inter * h // 2 + 2 * inter * (h // 128) * 2 if spec["w4"] else 2 * inter * h * 2
+    return e * (gu + h * inter * 2)
+
+
+def build_plans(spec, device):
+    """Prepared layers sharing inputs, each with its own weight copy.  Enough
+    copies rotate through the graphs that the set of weights they touch is at
+    least 1.5 x the Infinity Cache (a cyclic walk over more than the cache
+    finds nothing of the previous forward in it), at most 8 (one graph's
+    forwards); a workload whose 8 copies still fit is marked cache-resident."""
     from llm_gpu_kernels_amd import prepare_routed_moe, quantize_gate_up, tile_gate_up
     from llm_gpu_kernels_amd.workloads import make_layer
     lay = make_layer(spec["shape"], spec["T"], routing=spec["routing"], seed=0, device=device)
     gate_up = lay["gate_up"]
     if spec["w4"]:
         gate_up = tile_gate_up(quantize_gate_up(gate_up.cpu())).to(device)
+    one = weight_bytes(spec, lay)
+    copies = min(MAX_COPIES, max(2, -(-(3 * MALL_BYTES // 2) // one)))
+    lay["weight_copies"] = copies
+    lay["cache_resident"] = copies * one < 3 * MALL_BYTES // 2
     plans = []
     for c in range(copies):
         if c == 0:
@@ -94,17 +114,15 @@ def algorithmic(spec, lay, plan):
                 flops=flops, gate_up_flops=4 * t * k * h * inter)
 
 
-FORWARDS_PER_GRAPH = 8
-
-
 def time_layer(plans, steps, warmup):
     """Time exactly `steps` forwards; returns (ms per forward, per-graph samples).
 
     BASELINE's protocol (benchmark.py:68-98 of the reference): HIP graphs of
     FORWARDS_PER_GRAPH forwards, device time from HIP events on the replay
-    stream.  Two graphs alternate the two weight copies in opposite orders
-    (A B A B ... and B A B A ...), and replays alternate between them (AB/BA
-    rounds), so neither copy always runs first.  A third graph holds the
+    stream.  Two graphs cycle through the weight copies, one starting at copy
+    0 and one at copy 1 (A B A B ... and B A B A ... with two copies), and
+    replays alternate between them (AB/BA rounds), so no copy always runs
+    first.  A third graph holds the
     remainder steps % 8.  Warmup replays at least max(W, 32) forwards so the
     timed region starts at steady clocks.  Every full replay inside the timed
     region is also an event-timed sample (/8), and 16 more replays after it
@@ -203,7 +221,9 @@ def measure(name, steps, warmup, device):
         p95_us=round(sorted(samples)[int(0.95 * (len(samples) - 1))] * 1e3, 2),
         tokens_per_s=round(t / (ms * 1e-3), 1), active_experts=alg["active_experts"],
         layer_bytes=alg["layer_bytes"], layer_hbm_gbs=round(layer_gbs, 1),
-        layer_hbm_frac=round(layer_gbs / HBM_PEAK_GBS, 4),
+        weight_copies=lay["weight_copies"], cache_resident=lay["cache_resident"],
+        # A cache-resident workload's bytes per second are not HBM bandwidth.
+        layer_hbm_frac=None if lay["cache_resident"] else round(layer_gbs / HBM_PEAK_GBS, 4),
         layer_tflops=round(tflops, 2), mfma_frac=round(tflops / BF16_PEAK_TFLOPS, 4),
         attainable_roofline_frac=round(tflops / attainable, 4),
         stage_us=stage_ms,

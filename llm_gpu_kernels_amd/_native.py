@@ -8,7 +8,12 @@ import ctypes
 from ctypes import c_int32, c_size_t, c_uint32, c_void_p, POINTER
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmoe_mi355x.so"
+import os
+
+# MOE_MI355X_LIB names another build of the same library (A/B measurements of
+# a variant without replacing the in-tree one); the default is the in-tree build.
+LIB_PATH = Path(os.environ.get("MOE_MI355X_LIB") or
+                Path(__file__).resolve().parent / "_lib" / "libmoe_mi355x.so")
 
 MOE_OK, MOE_EINVAL, MOE_EDEVICE, MOE_ESPACE = 0, -1, -2, -3
 WEIGHTS_BF16, WEIGHTS_W4G128, WEIGHTS_W4G128_FOLD = 0, 1, 2

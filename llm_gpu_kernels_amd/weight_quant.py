@@ -88,28 +88,69 @@ class RepackedGateUp:
         return RepackedGateUp(self.words.to(device), self.scales.to(device), self.metadata)
 
 
+def _check_v1(packed: PackedGateUp) -> tuple:
+    """Digests of a v1 pack, verified against its metadata when recorded
+    (moe_weight_layout.py:60-78): a pack whose bits differ from its recorded
+    words_sha256 / scales_sha256 is rejected, not rearranged."""
+    meta = packed.metadata or {}
+    if meta:
+        if meta.get("format_version", 1) != 1 or meta.get("group_size", GROUP) != GROUP:
+            raise ValueError("v1 metadata must declare format_version=1 and group_size=128")
+        if "logical_shape" in meta and tuple(meta["logical_shape"]) != tuple(packed.shape):
+            raise ValueError("v1 metadata logical_shape does not match the buffers")
+    words_sha, scales_sha = _digest(packed.words), _digest(packed.scales)
+    for key, got in (("words_sha256", words_sha), ("scales_sha256", scales_sha)):
+        if key in meta and meta[key] != got:
+            raise ValueError(f"v1 packed buffers do not match their recorded {key}")
+    return words_sha, scales_sha
+
+
 def repack_gate_up(packed: PackedGateUp) -> RepackedGateUp:
     """v1 -> M24, a pure permutation of words and scales (moe_weight_layout.py:81-88):
     v1 word [e, p*(N/2) + t*64 + l, 4*k + w] -> [e, p, t, k, w, l]; v1 scale
-    [e, p*(N/2) + t*64 + l, g] -> [e, p, t, g, l]."""
+    [e, p*(N/2) + t*64 + l, g] -> [e, p, t, g, l].  The metadata carries what the
+    reference's restore_v1_layout checks (moe_weight_layout.py:130-175): the
+    physical and canonical digests and a v1 metadata snapshot whose digests
+    match the canonical ones, plus the byte ledger (moe_weight_layout.py:90-121)."""
     e, n, k = packed.shape
     if n % (2 * M24_LANES) or k % GROUP:
         raise ValueError("M24 layout needs N % 128 == 0 and K % 128 == 0")
+    words_sha, scales_sha = _check_v1(packed)
     nt = n // (2 * M24_LANES)
     words = packed.words.reshape(e, 2, nt, M24_LANES, k // 32, 4).permute(0, 1, 2, 4, 5, 3)
     scales = packed.scales.reshape(e, 2, nt, M24_LANES, k // GROUP).permute(0, 1, 2, 4, 3)
     words, scales = words.contiguous(), scales.contiguous()
+    v1_meta = dict(packed.metadata or {})
+    v1_meta.setdefault("format_version", 1)
+    v1_meta.setdefault("group_size", GROUP)
+    v1_meta.setdefault("logical_shape", [e, n, k])
+    v1_meta["words_sha256"], v1_meta["scales_sha256"] = words_sha, scales_sha
+    wb, sb = packed.words.numel() * 4, packed.scales.numel() * 2
     meta = dict(format_version=2, layout=M24_LAYOUT, logical_shape=[e, n, k], group_size=GROUP,
-                canonical_v1_metadata=dict(packed.metadata),
+                canonical_words_sha256=words_sha, canonical_scales_sha256=scales_sha,
+                canonical_words_shape=list(packed.words.shape),
+                canonical_scales_shape=list(packed.scales.shape),
                 physical_words_shape=list(words.shape), physical_scales_shape=list(scales.shape),
-                physical_words_sha256=_digest(words), physical_scales_sha256=_digest(scales))
+                physical_words_sha256=_digest(words), physical_scales_sha256=_digest(scales),
+                canonical_v1_metadata=v1_meta,
+                byte_ledger=dict(canonical_words_bytes=wb, canonical_scales_bytes=sb,
+                                 canonical_packed_total_bytes=wb + sb,
+                                 physical_words_bytes=wb, physical_scales_bytes=sb,
+                                 physical_packed_total_bytes=wb + sb,
+                                 additional_repacked_tensor_bytes=wb + sb,
+                                 canonical_plus_repacked_resident_bytes=2 * (wb + sb),
+                                 physical_packed_total_mib=(wb + sb) / (1024 * 1024),
+                                 interpretation="layout-only storage; quantization and total "
+                                                "packed bytes are unchanged"))
     return RepackedGateUp(words, scales, meta)
 
 
 def restore_v1_layout(repacked: RepackedGateUp) -> PackedGateUp:
     """M24 -> v1 with the original bit patterns (inverse permutation of
     moe_weight_layout.py:85-88).  Metadata, when present, must declare the M24
-    layout (moe_weight_layout.py:134-141); recorded physical digests are checked."""
+    layout (moe_weight_layout.py:134-141); every recorded digest is checked:
+    the physical ones before the permutation, the canonical ones after it, and
+    the v1 snapshot's digests against the canonical ones (:150-174)."""
     meta = repacked.metadata or {}
     if meta and (meta.get("format_version") != 2 or meta.get("layout") != M24_LAYOUT
                  or meta.get("group_size", GROUP) != GROUP):
@@ -125,9 +166,25 @@ def restore_v1_layout(repacked: RepackedGateUp) -> PackedGateUp:
             raise ValueError(f"M24 buffer does not match its recorded {key}")
     e, p, nt, k32, _, nl = words.shape
     n, k = p * nt * nl, k32 * 32
+    if "logical_shape" in meta and tuple(meta["logical_shape"]) != (e, n, k):
+        raise ValueError("M24 metadata logical_shape does not match the buffers")
     v1_words = words.permute(0, 1, 2, 5, 3, 4).reshape(e, n, k // 8).contiguous()
     v1_scales = scales.permute(0, 1, 2, 4, 3).reshape(e, n, k // GROUP).contiguous()
-    return PackedGateUp(v1_words, v1_scales, dict(meta.get("canonical_v1_metadata", {})))
+    canon = {}
+    for key, t in (("canonical_words_sha256", v1_words), ("canonical_scales_sha256", v1_scales)):
+        if key in meta:
+            canon[key] = _digest(t)
+            if canon[key] != meta[key]:
+                raise ValueError("restored v1 bit patterns do not match the canonical digests")
+    v1_meta = dict(meta.get("canonical_v1_metadata", {}) or {})
+    if v1_meta:
+        if v1_meta.get("format_version", 1) != 1 or v1_meta.get("group_size", GROUP) != GROUP:
+            raise ValueError("M24 metadata has no matching canonical v1 metadata snapshot")
+        for v1_key, key in (("words_sha256", "canonical_words_sha256"),
+                            ("scales_sha256", "canonical_scales_sha256")):
+            if v1_key in v1_meta and key in meta and v1_meta[v1_key] != meta[key]:
+                raise ValueError("M24 metadata has no matching canonical v1 metadata snapshot")
+    return PackedGateUp(v1_words, v1_scales, v1_meta)
 
 
 def quantize_gate_up(weight: torch.Tensor) -> PackedGateUp:
@@ -155,6 +212,8 @@ def tile_gate_up(packed) -> TiledGateUp:
     """Rearrange v1 (or M24) words/scales (any device) into the gfx950 layout on the host."""
     if isinstance(packed, RepackedGateUp):
         packed = restore_v1_layout(packed.to("cpu"))
+    elif isinstance(packed, PackedGateUp) and packed.metadata:
+        _check_v1(packed.to("cpu"))
     words = packed.words.detach().cpu().contiguous()
     scales = packed.scales.detach().cpu().contiguous()
     e, n, k = packed.shape

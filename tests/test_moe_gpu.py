@@ -220,6 +220,33 @@ def test_routed_w4_fold_layer(tokens, gpu_device):
         prepare_routed_moe(lay["x"], lay["logits"], tiled, lay["down"], lay["K"], w4_decode="bf16")
 
 
+@pytest.mark.parametrize("shift", ["x+3", "abs(x)+1", "x+16"])
+def test_w4_fold_offset_heavy_inputs(shift, gpu_device):
+    """The folded decode computes scale * (sum((136 + q) x) - 136 sum(x)) per
+    128-K group in fp32, so its rounding error grows with the common offset of
+    x (the two terms cancel).  With activations shifted away from zero it stays
+    within the layer tolerance of the FP32 oracle on the unrounded weights;
+    the printed errors are the bound recorded for the fold mode."""
+    lay = make_layer("qwen", 17, seed=0, device=gpu_device)
+    x = lay["x"].float()
+    x = {"x+3": x + 3.0, "abs(x)+1": x.abs() + 1.0, "x+16": x + 16.0}[shift].to(torch.bfloat16)
+    packed = quantize_gate_up(lay["gate_up"].cpu())
+    tiled = tile_gate_up(packed).to(gpu_device)
+    plan = prepare_routed_moe(x, lay["logits"], tiled, lay["down"], lay["K"], w4_decode="fold")
+    out = plan.forward(x, lay["logits"])
+    torch.cuda.synchronize()
+    ids, w = O.route_topk(lay["logits"].cpu(), lay["K"])
+    un = O.dequantize_w4_unrounded(packed.words, packed.scales)
+    m = O.error(out, O.moe_reference(x.cpu(), un, lay["down"].cpu(), ids, w))
+    exact = prepare_routed_moe(x, lay["logits"], tiled, lay["down"], lay["K"])
+    ex = exact.forward(x, lay["logits"])
+    torch.cuda.synchronize()
+    me = O.error(ex, O.moe_reference(x.cpu(), O.dequantize_w4(packed.words, packed.scales),
+                                     lay["down"].cpu(), ids, w))
+    print(f"fold {shift}: {m}  exact: {me}")
+    assert m["passed"], m
+
+
 # One GPU's share of the Qwen layer under 8-way expert parallelism (16 experts,
 # one route per row: the streaming and the tiled kernels) and tensor parallelism
 # (I = 96: the run-time-K kernels), as the bench measures them.

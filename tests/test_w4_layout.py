@@ -86,3 +86,71 @@ def test_tiling_from_m24_equals_tiling_from_v1():
     b = tile_gate_up(repack_gate_up(packed))
     assert torch.equal(a.words, b.words)
     assert torch.equal(a.scales.view(torch.int16), b.scales.view(torch.int16))
+
+
+def _reference_restore_accepts(rep):
+    """The metadata conditions of the reference's restore_v1_layout
+    (moe_weight_layout.py:130-175), restated as checks on a pack this library
+    wrote: layout declaration, physical digests of the buffers, canonical
+    digests of the restored v1 bits, and a v1 snapshot carrying them."""
+    from llm_gpu_kernels_amd.weight_quant import _digest
+    meta = rep.metadata
+    assert meta["format_version"] == 2 and meta["layout"] == M24_LAYOUT
+    assert meta["group_size"] == 128 and tuple(meta["logical_shape"]) == rep.shape
+    assert _digest(rep.words) == meta["physical_words_sha256"]
+    assert _digest(rep.scales) == meta["physical_scales_sha256"]
+    back = restore_v1_layout(rep)
+    assert _digest(back.words) == meta["canonical_words_sha256"]
+    assert _digest(back.scales) == meta["canonical_scales_sha256"]
+    v1 = meta["canonical_v1_metadata"]
+    assert v1["format_version"] == 1 and v1["group_size"] == 128
+    assert tuple(v1["logical_shape"]) == rep.shape
+    assert v1["words_sha256"] == meta["canonical_words_sha256"]
+    assert v1["scales_sha256"] == meta["canonical_scales_sha256"]
+    led = meta["byte_ledger"]
+    assert led["physical_packed_total_bytes"] == led["canonical_packed_total_bytes"]
+    return back
+
+
+def test_m24_export_carries_what_reference_restore_checks():
+    # The audited shape: 192 MiB of words + 6 MiB of scales = 198 MiB
+    # (moe_weight_layout.py:119-120), v1 metadata as quantize_gate_up writes it.
+    from llm_gpu_kernels_amd.weight_quant import _digest
+    g = torch.Generator().manual_seed(9)
+    words = torch.randint(-2**31, 2**31 - 1, (128, 1536, 256), generator=g, dtype=torch.int32)
+    scales = torch.rand((128, 1536, 16), generator=g).to(torch.bfloat16)
+    v1 = dict(format_version=1, logical_shape=[128, 1536, 2048], group_size=128,
+              words_sha256=_digest(words), scales_sha256=_digest(scales))
+    rep = repack_gate_up(PackedGateUp(words, scales, v1))
+    assert tuple(rep.words.shape) == (128, 2, 12, 64, 4, 64)
+    assert tuple(rep.scales.shape) == (128, 2, 12, 16, 64)
+    assert rep.metadata["byte_ledger"]["physical_packed_total_mib"] == 198.0
+    back = _reference_restore_accepts(rep)
+    assert torch.equal(back.words, words)
+    assert back.metadata["words_sha256"] == v1["words_sha256"]
+
+
+def test_v1_digests_checked_on_import_and_restore():
+    from llm_gpu_kernels_amd import quantize_gate_up
+    g = torch.Generator().manual_seed(6)
+    w = (torch.randn((2, 256, 256), generator=g) * 0.02).to(torch.bfloat16)
+    packed = quantize_gate_up(w)
+    _reference_restore_accepts(repack_gate_up(packed))
+    bad = packed.words.clone()
+    bad[0, 0, 0] ^= 0x10
+    tampered = PackedGateUp(bad, packed.scales, packed.metadata)
+    with pytest.raises(ValueError, match="words_sha256"):
+        tile_gate_up(tampered)
+    with pytest.raises(ValueError, match="words_sha256"):
+        repack_gate_up(tampered)
+    with pytest.raises(ValueError):
+        tile_gate_up(PackedGateUp(packed.words, packed.scales, dict(packed.metadata, format_version=3)))
+    rep = repack_gate_up(packed)
+    # A physical pack consistent with its physical digests but not with the
+    # canonical ones, or with a v1 snapshot of other bits, is refused.
+    for key in ("canonical_words_sha256", "canonical_scales_sha256"):
+        with pytest.raises(ValueError, match="canonical"):
+            restore_v1_layout(RepackedGateUp(rep.words, rep.scales, dict(rep.metadata, **{key: "0" * 64})))
+    snap = dict(rep.metadata["canonical_v1_metadata"], words_sha256="f" * 64)
+    with pytest.raises(ValueError, match="snapshot"):
+        restore_v1_layout(RepackedGateUp(rep.words, rep.scales, dict(rep.metadata, canonical_v1_metadata=snap)))
