@@ -122,7 +122,7 @@ bool planned_gate_up(const moe_desc *d, int path, int tb) {
 constexpr int kAssumedCUs = 256;  // MI355X; plans use the device's own count
 bool multi_planner(const moe_desc *d, int path, int tb, int num_cus) {
   if (planned_gate_up(d, path, tb) || fuse_router_mode(d) != 0) return false;
-  return moe::multi_plan_ok(d->T, d->K, d->route_mode == MOE_ROUTE_LOGITS, num_cus);
+  return moe::multi_plan_ok(d->T, d->K, d->E, d->route_mode == MOE_ROUTE_LOGITS, num_cus);
 }
 
 int launch_count(const moe_desc *d, int path, int tb, int num_cus) {
@@ -158,7 +158,7 @@ moe_layout compute_layout(const moe_desc *d) {
   L.tasks = take(cap * 16);
   L.num_tasks = take(4);
   {
-    const int tpw = moe::multi_plan_tokens(d->K, d->route_mode == MOE_ROUTE_LOGITS);
+    const int tpw = moe::multi_plan_tokens(d->K, d->E, d->route_mode == MOE_ROUTE_LOGITS);
     const size_t W = tpw > 0 ? ((size_t)d->T + tpw - 1) / tpw : 0;
     L.partials = take(W * ((size_t)d->E + 1) * 4 + 4);  // + the planner's arrival counter
   }
@@ -346,7 +346,7 @@ static int run_stages(moe_plan *p, int first, int last, void *stream) {
   ra.fuse_router = p->fuse_router;
   ra.token_block = L.token_block;
   ra.partials = (int32_t *)(ws + L.partials);
-  ra.plan_tpw = moe::multi_plan_tokens(d.K, ra.route_logits);
+  ra.plan_tpw = moe::multi_plan_tokens(d.K, d.E, ra.route_logits);
   ra.plan_spin_cap = moe::kMultiSpinCap;
   ra.plan_hold_wg = -1;
   // Test hook (failure-handling tests only): the last planner workgroup

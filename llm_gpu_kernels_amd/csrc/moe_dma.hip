@@ -193,6 +193,8 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     int *x_toff = x_off + kMaxExperts;
     uint32_t *x_flags = (uint32_t *)(x_toff + kMaxExperts + 1);
     // One token per wave (fuse_router 1) or half-wave (2); logits first.
+    // (16 lanes per token measured 0.4 us slower here: the sixteen waves
+    // route up to 32 tokens in one pass either way.)
     const bool half = ra.fuse_router == 2;
     const int ft = half ? 2 * wave + (lane >> 5) : wave;
     const bool fwave = half ? 2 * wave < ra.T : wave < ra.T;  // wave-uniform

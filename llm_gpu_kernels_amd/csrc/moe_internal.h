@@ -58,8 +58,8 @@ hipError_t launch_router(const RouteArgs &a, hipStream_t s);
 // Single-workgroup planner (fuses the router when a.fuse_router).
 hipError_t launch_route_plan(const RouteArgs &a, hipStream_t s);
 // Multi-workgroup router + planner (a.plan_tpw tokens per workgroup).
-int multi_plan_tokens(int K, bool router);
-bool multi_plan_ok(int T, int K, bool router, int num_cus);
+int multi_plan_tokens(int K, int E, bool router);
+bool multi_plan_ok(int T, int K, int E, bool router, int num_cus);
 hipError_t launch_route_plan_multi(const RouteArgs &a, hipStream_t s);
 
 // token_block: 16 or 32 grouped rows per task.  fast: MFMA kernels (shape

@@ -364,10 +364,11 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   // epoch word, whose device-coherent load is another memory round trip:
   // the two overlap instead of the logits waiting behind it.  With E <= 128
   // each token is routed by a half-wave, so the chunk's 16 tokens take 8
-  // waves (2 per SIMD) instead of 16: the routing chains are bound by SIMD
-  // issue, and this halves it.
-  float raw[4];
+  // waves; else one token per wave.  (16 lanes per token, with 16, 32 or 64
+  // tokens per workgroup, measured 0.3-2 us slower at T = 193 and no faster
+  // at T = 1024: this launch is bound by latency, not by issue.)
   const bool half = ROUTER && E <= 128;
+  float raw[4];
   const int rt = half ? t0 + 2 * wave + (lane >> 5) : t0 + wave;
   if (ROUTER) {
     if (half) load_token_logits<true>(a.logits, rt, rt < t1, E, raw);
@@ -382,9 +383,9 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   uint32_t flags = 0;
   if constexpr (ROUTER) {
     if (half) {
-      if (t0 + 2 * wave < t1)  // wave-uniform: the wave's first token exists
-        route_token<true>(raw, rt, rt < t1, E, K, a.renormalize, (int32_t *)a.ids, a.weights,
-                          flags, s_ids - q0, s_w - q0);
+      if (t0 + 2 * wave < t1)
+        route_token<true>(raw, rt, rt < t1, E, K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
+                          s_ids - q0, s_w - q0);
     } else if (rt < t1) {
       route_token<false>(raw, rt, true, E, K, a.renormalize, (int32_t *)a.ids, a.weights, flags,
                          s_ids - q0, s_w - q0);
@@ -596,12 +597,15 @@ hipError_t launch_router(const RouteArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-bool multi_plan_ok(int T, int K, bool router, int num_cus) {
-  const int tpw = multi_plan_tokens(K, router);
+bool multi_plan_ok(int T, int K, int E, bool router, int num_cus) {
+  const int tpw = multi_plan_tokens(K, E, router);
   return T > 0 && tpw > 0 && (T + tpw - 1) / tpw <= num_cus && num_cus <= 4096;
 }
 
-int multi_plan_tokens(int K, bool router) {
+// Tokens per planner workgroup: with the router 16 (one per wave or
+// half-wave); fixed routes 1024 / K (one route per thread).
+int multi_plan_tokens(int K, int E, bool router) {
+  (void)E;
   if (router) return K <= kMultiThreads / kMultiWaves ? kMultiWaves : 0;
   return K <= kMultiThreads ? kMultiThreads / K : 0;
 }

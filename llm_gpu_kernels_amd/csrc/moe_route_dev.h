@@ -28,24 +28,30 @@ __device__ __forceinline__ float key_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Reductions over the lanes routing one token: the whole wave (HALF =
-// false) or each 32-lane half (HALF = true): DPP within 16-lane rows, then
-// gfx950's row-pair and half swaps; every lane of the group gets the result.
-// The float sum adds rows as (r0 + r1) + (r2 + r3).
-template <bool HALF>
-__device__ __forceinline__ float group_fsum(float x) {
+// Reductions over the L lanes routing one token (L = 64, 32 or 16): DPP
+// within 16-lane rows, then gfx950's row-pair and half swaps; every lane of
+// the group gets the result.  The float sum adds rows as (r0 + r1) + (r2 + r3).
+template <int L>
+__device__ __forceinline__ float group_fsum_l(float x) {
+  static_assert(L == 16 || L == 32 || L == 64, "lanes per token");
   uint32_t v = __float_as_uint(x);
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0xb1>(v)));
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x4e>(v)));
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x141>(v)));
   v = __float_as_uint(__uint_as_float(v) + __uint_as_float(dpp_u<0x140>(v)));
-  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = __float_as_uint(__uint_as_float(q[0]) + __uint_as_float(q[1]));
-  if (!HALF) {
+  if (L >= 32) {
+    const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = __float_as_uint(__uint_as_float(q[0]) + __uint_as_float(q[1]));
+  }
+  if (L == 64) {
     const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
     v = __float_as_uint(__uint_as_float(h[0]) + __uint_as_float(h[1]));
   }
   return __uint_as_float(v);
+}
+template <bool HALF>
+__device__ __forceinline__ float group_fsum(float x) {
+  return group_fsum_l<HALF ? 32 : 64>(x);
 }
 // Inclusive prefix sum over the wave: DPP row shifts, then row broadcasts
 // (lane 15 into rows 1 and 3, lane 31 into rows 2 and 3).
@@ -64,35 +70,49 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return v;
 }
 
-template <bool HALF, bool MAX>
-__device__ __forceinline__ uint32_t group_uext(uint32_t v) {
+template <int L, bool MAX>
+__device__ __forceinline__ uint32_t group_uext_l(uint32_t v) {
+  static_assert(L == 16 || L == 32 || L == 64, "lanes per token");
   auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
   v = op(v, dpp_u<0xb1>(v));
   v = op(v, dpp_u<0x4e>(v));
   v = op(v, dpp_u<0x141>(v));
   v = op(v, dpp_u<0x140>(v));
-  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = op(q[0], q[1]);
-  if (!HALF) {
+  if (L >= 32) {
+    const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(q[0], q[1]);
+  }
+  if (L == 64) {
     const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
     v = op(h[0], h[1]);
   }
   return v;
 }
+template <bool HALF, bool MAX>
+__device__ __forceinline__ uint32_t group_uext(uint32_t v) {
+  return group_uext_l<HALF ? 32 : 64, MAX>(v);
+}
 
-// Logits of token t for one lane: expert e = h + L j (j < 4) with L = 64
-// lanes per token (h = lane) or L = 32 (HALF: h = lane % 32, token of the
-// half).  Issued early so the planner's set-up hides their latency.
-template <bool HALF>
-__device__ __forceinline__ void load_token_logits(const float *__restrict__ logits, int t, bool live,
-                                                  int E, float (&raw)[4]) {
-  constexpr int L = HALF ? 32 : 64;
+// Logits of token t for one lane: expert e = h + L j (j < KPL) with L lanes
+// per token, h = lane % L: L = 64 or 32 with four logits per lane (E <= 256
+// and E <= 128), L = 16 with eight (E <= 128).  Issued early so the
+// planner's set-up hides their latency.
+template <int L>
+constexpr int kKeysPerLane = L == 16 ? 8 : 4;
+template <int L>
+__device__ __forceinline__ void load_token_logits_l(const float *__restrict__ logits, int t, bool live,
+                                                    int E, float (&raw)[kKeysPerLane<L>]) {
   const int h = threadIdx.x & (L - 1);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kKeysPerLane<L>; ++j) {
     const int e = h + L * j;
     raw[j] = live && e < E ? logits[(size_t)t * E + e] : -INFINITY;
   }
+}
+template <bool HALF>
+__device__ __forceinline__ void load_token_logits(const float *__restrict__ logits, int t, bool live,
+                                                  int E, float (&raw)[4]) {
+  load_token_logits_l<HALF ? 32 : 64>(logits, t, live, E, raw);
 }
 
 // The lanes of one token route it from its logits (raw, as loaded above).
@@ -106,66 +126,114 @@ __device__ __forceinline__ void load_token_logits(const float *__restrict__ logi
 // when `lds_ids` is given, to LDS for the planner (global memory only when
 // `ids_out` is non-null).  A group with live ==
 // false computes on nothing and stores nothing.
-template <bool HALF>
-__device__ void route_token(const float (&raw)[4], int t, bool live, int E, int K, int renormalize,
-                            int32_t *__restrict__ ids_out, float *__restrict__ w_out,
-                            uint32_t &flags, int *lds_ids, float *lds_w) {
-  constexpr int L = HALF ? 32 : 64;
+template <int L, int NT>
+__device__ void route_tokens(const float (&raw)[NT][kKeysPerLane<L>], const int (&t)[NT], const bool (&live)[NT], int E,
+                             int K, int renormalize, int32_t *__restrict__ ids_out,
+                             float *__restrict__ w_out, uint32_t &flags, int *lds_ids, float *lds_w) {
+  // NT tokens per lane group, their dependency chains interleaved step by
+  // step (every loop below runs over the tokens innermost), so a group
+  // routing two tokens takes about the latency of one.
+  constexpr int KPL = kKeysPerLane<L>;
   const int h = threadIdx.x & (L - 1);
-  uint32_t key[4];
+  uint32_t key[NT][KPL];
   bool bad = false;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool ok = live && h + L * j < E;
-    bad |= ok && !isfinite(raw[j]);
-    key[j] = ok ? float_key(raw[j]) + 1u : 0u;
-  }
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const bool ok = live[n] && h + L * j < E;
+      bad |= ok && !isfinite(raw[n][j]);
+      key[n][j] = ok ? float_key(raw[n][j]) + 1u : 0u;
+    }
   if (__any(bad)) flags |= 4u;
-  auto top4 = [&]() {
-    const uint32_t a = key[0] > key[1] ? key[0] : key[1], b = key[2] > key[3] ? key[2] : key[3];
-    return a > b ? a : b;
+  auto top4 = [&](int n) {  // the lane's best remaining key (pairwise tree)
+    uint32_t v[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) v[j] = key[n][j];
+#pragma unroll
+    for (int w = KPL / 2; w > 0; w /= 2)
+#pragma unroll
+      for (int j = 0; j < w; ++j) v[j] = v[j] > v[j + w] ? v[j] : v[j + w];
+    return v[0];
   };
-  const uint32_t kmax = group_uext<HALF, true>(top4());
-  const float m = key_float(kmax - 1u);
-  float z = 0.f;
+  float m[NT], z[NT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (live && h + L * j < E) z += expf(raw[j] - m);
-  z = group_fsum<HALF>(z);
+  for (int n = 0; n < NT; ++n) m[n] = key_float(group_uext_l<L, true>(top4(n)) - 1u);
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    z[n] = 0.f;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j)
+      if (live[n] && h + L * j < E) z[n] += expf(raw[n][j] - m[n]);
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n) z[n] = group_fsum_l<L>(z[n]);
 
-  uint32_t my_key = 1;
-  int my_id = kMaxExperts;
+  uint32_t my_key[NT];
+  int my_id[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    my_key[n] = 1;
+    my_id[n] = kMaxExperts;
+  }
   for (int k = 0; k < K; ++k) {
-    const uint32_t M = group_uext<HALF, true>(top4());
-    uint32_t c = kMaxExperts;
+    uint32_t M[NT], c[NT];
 #pragma unroll
-    for (int j = 3; j >= 0; --j)
-      if (M != 0 && key[j] == M) c = h + L * j;
-    const int idx = (int)group_uext<HALF, false>(c);
-    if (idx < kMaxExperts && (idx & (L - 1)) == h) {
+    for (int n = 0; n < NT; ++n) M[n] = group_uext_l<L, true>(top4(n));
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (idx / L == j) key[j] = 0;
+    for (int n = 0; n < NT; ++n) {
+      c[n] = kMaxExperts;
+#pragma unroll
+      for (int j = KPL - 1; j >= 0; --j)
+        if (M[n] != 0 && key[n][j] == M[n]) c[n] = h + L * j;
     }
-    if (h == k) {
-      my_key = M;
-      my_id = idx;
+    int idx[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) idx[n] = (int)group_uext_l<L, false>(c[n]);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      if (idx[n] < kMaxExperts && (idx[n] & (L - 1)) == h) {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j)
+          if (idx[n] / L == j) key[n][j] = 0;
+      }
+      if (h == k) {
+        my_key[n] = M[n];
+        my_id[n] = idx[n];
+      }
     }
   }
-  const float p = h < K ? expf(key_float(my_key - 1u) - m) / z : 0.f;
-  const float psum = group_fsum<HALF>(p);
-  if (live && h < K) {
-    const int q = t * K + h;
-    const float w = renormalize ? p / psum : p;
-    if (ids_out) {
-      ids_out[q] = my_id;
-      w_out[q] = w;
-    }
-    if (lds_ids) {
-      lds_ids[q] = my_id;
-      lds_w[q] = w;
+  float p[NT], psum[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) p[n] = h < K ? expf(key_float(my_key[n] - 1u) - m[n]) / z[n] : 0.f;
+#pragma unroll
+  for (int n = 0; n < NT; ++n) psum[n] = group_fsum_l<L>(p[n]);
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    if (live[n] && h < K) {
+      const int q = t[n] * K + h;
+      const float w = renormalize ? p[n] / psum[n] : p[n];
+      if (ids_out) {
+        ids_out[q] = my_id[n];
+        w_out[q] = w;
+      }
+      if (lds_ids) {
+        lds_ids[q] = my_id[n];
+        lds_w[q] = w;
+      }
     }
   }
+}
+
+template <bool HALF>
+__device__ __forceinline__ void route_token(const float (&raw)[4], int t, bool live, int E, int K,
+                                            int renormalize, int32_t *__restrict__ ids_out,
+                                            float *__restrict__ w_out, uint32_t &flags, int *lds_ids,
+                                            float *lds_w) {
+  const float (&r1)[1][4] = *reinterpret_cast<const float(*)[1][4]>(&raw);
+  const int t1[1] = {t};
+  const bool l1[1] = {live};
+  route_tokens<HALF ? 32 : 64, 1>(r1, t1, l1, E, K, renormalize, ids_out, w_out, flags, lds_ids, lds_w);
 }
 
 

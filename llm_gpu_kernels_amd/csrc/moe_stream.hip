@@ -81,6 +81,15 @@ constexpr size_t stream_lds(bool plan) {
          (FOLD ? (size_t)kWaves * (SPW / 4) * MT * 16 * sizeof(float) : 0) + (plan ? kPlanLds : 0);
 }
 
+#ifdef MOE_EXP_STAMPS
+#define STAMP(k)                                                                              \
+  do {                                                                                        \
+    if (PLAN && blockIdx.x < 64 && threadIdx.x == 0)                                          \
+      ((uint64_t *)a.routed)[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime();      \
+  } while (0)
+#else
+#define STAMP(k) do {} while (0)
+#endif
 template <int KIND, int MT, int SPW, bool W4, bool FOLD, bool PLAN = false>
 __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertArgs a, RouteArgs ra) {
   constexpr int NRB = 2;
@@ -97,6 +106,7 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
   const int4 *l_tasks = nullptr;
   const int *l_row = nullptr;
   int ntasks = 0;
+  STAMP(0);
   if constexpr (PLAN) {
     using namespace route_dev;
     uint8_t *pl = (uint8_t *)s_red + stream_lds<KIND, MT, SPW, W4, FOLD>(false);
@@ -111,40 +121,67 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
     int *x_off = x_cnt + kMaxExperts;
     int *x_toff = x_off + kMaxExperts;
     uint32_t *x_flags = (uint32_t *)(x_toff + kMaxExperts + 1);
-    // One token per wave (fuse_router 1, T <= 16) or half-wave (2, T <= 32):
-    // two rounds of the eight waves; every round's logits are requested first.
-    const bool half = ra.fuse_router == 2;
-    const int per_round = half ? 2 * kWaves : kWaves;
+    // Routing: with E <= 128 and K <= 16, 16 lanes per token (eight logits
+    // per lane), so the eight waves route up to 32 tokens in one pass; the
+    // prologue's routing is bound by instruction issue (every workgroup routes
+    // every token), and 16-lane groups need about 2.4x fewer wave
+    // instructions than half-waves over two rounds.  Otherwise one token per
+    // wave (T <= 16), two per wave interleaved.  All logits are requested
+    // before the LDS set-up.
+    const bool quarter = ra.E <= 128 && ra.K <= 16;
+    const bool half = !quarter && ra.fuse_router == 2;  // K > 16, T <= 32: 32 lanes per token
+    const int per_pass = half ? 2 * kWaves : kWaves;
+    float rq[1][8];
     float raw[2][4];
     int ft[2];
+    if (quarter) {
+      ft[0] = 4 * wave + (lane >> 4);
+      load_token_logits_l<16>(ra.logits, ft[0], ft[0] < ra.T, ra.E, rq[0]);
+    } else {
 #pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-      ft[rd] = rd * per_round + (half ? 2 * wave + (lane >> 5) : wave);
-      if (half) load_token_logits<true>(ra.logits, ft[rd], ft[rd] < ra.T, ra.E, raw[rd]);
-      else load_token_logits<false>(ra.logits, ft[rd], ft[rd] < ra.T, ra.E, raw[rd]);
+      for (int rd = 0; rd < 2; ++rd) {
+        ft[rd] = rd * per_pass + (half ? 2 * wave + (lane >> 5) : wave);
+        if (half) load_token_logits<true>(ra.logits, ft[rd], ft[rd] < ra.T, ra.E, raw[rd]);
+        else load_token_logits<false>(ra.logits, ft[rd], ft[rd] < ra.T, ra.E, raw[rd]);
+      }
     }
     for (int i = tid; i < kWaves * ra.E; i += kThreads) x_wcnt[i] = 0;
     if (tid == 0) *x_flags = 0;
+#ifdef MOE_EXP_STAMPS
+    __builtin_amdgcn_s_waitcnt(0);
+    STAMP(4);
+#endif
     const bool g0 = blockIdx.x == 0;
     if (g0 && tid < 4) ra.counters[tid] = 0;
     uint32_t flags = 0;
     int32_t *ids_g = g0 ? (int32_t *)ra.ids : nullptr;
     float *w_g = g0 ? ra.weights : nullptr;
-#pragma unroll
-    for (int rd = 0; rd < 2; ++rd) {
-      const bool fwave = rd * per_round + (half ? 2 * wave : wave) < ra.T;  // wave-uniform
-      if (!fwave) continue;
-      if (half)
-        route_token<true>(raw[rd], ft[rd], ft[rd] < ra.T, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
-      else
-        route_token<false>(raw[rd], ft[rd], true, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+    if (quarter) {
+      if (4 * wave < ra.T) {  // wave-uniform: the wave's first token exists
+        const int t1[1] = {ft[0]};
+        const bool l1[1] = {ft[0] < ra.T};
+        route_tokens<16, 1>(rq, t1, l1, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+      }
+    } else {
+      // Up to two tokens per wave (or half-wave), routed in one interleaved pass.
+      const int first = half ? 2 * wave : wave;  // wave-uniform
+      const bool live2[2] = {ft[0] < ra.T, ft[1] < ra.T};
+      if (first + per_pass < ra.T) {
+        if (half) route_tokens<32, 2>(raw, ft, live2, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+        else route_tokens<64, 2>(raw, ft, live2, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+      } else if (first < ra.T) {
+        if (half) route_token<true>(raw[0], ft[0], live2[0], ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+        else route_token<false>(raw[0], ft[0], true, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
+      }
     }
     __syncthreads();
+    STAMP(1);
     const SmallPlanLds L{x_ids, x_w, x_wcnt, x_cnt, x_off, x_toff, p_tasks, p_row, p_nt, x_flags};
     const SmallPlanOut O{ra.counts, ra.offsets, ra.ranks, ra.map, ra.row_route, ra.row_token,
                          ra.tasks, ra.num_tasks, ra.status};
     plan_small<kThreads>(L, O, g0, ra.R, ra.E, ra.K, 16, flags);
     ntasks = *p_nt;
+    STAMP(2);
     l_tasks = p_tasks;
     l_row = p_row;
   }
@@ -266,7 +303,11 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
         const size_t rbi = (size_t)ex * (2 * I / 16) + cb + (rb ? I / 16 : 0);
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
+#ifdef MOE_EXP_NOLOAD
+          const size_t unit = (size_t)((s0 >> 2) + i) + (rb ? G4 : 0) + 0 * rbi;
+#else
           const size_t unit = rbi * G4 + (s0 >> 2) + i;
+#endif
           buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + lane];
           sc[rb][i] = a.w4_scales[unit * 16 + r];
         }
@@ -297,6 +338,7 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
     }
   }
   int btask = mq[0].task;
+  STAMP(3);
 
   int i = 0;
   int parity = 0;
@@ -344,7 +386,13 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
           const W4Scale ks = w4_scale(bf16_bits_to_f32(sq[SL][rb][i]));
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
+#ifdef MOE_EXP_NODECODE
+            const uint32_t wq = aq[SL][rb][i][j];
+            const u32x4 af = u32x4{wq, wq, wq, wq};
+            (void)ks;
+#else
             const u32x4 af = w4_decode8(aq[SL][rb][i][j], ks);
+#endif
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(af, bfr[mt][i * 4 + j], acc[rb][mt]);
           }
@@ -377,7 +425,9 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
         }
       }
 
+#ifndef MOE_EXP_NOBARRIER
     lds_barrier();
+#endif
 
     // Epilogue of cur: fixed-order sum of the eight K-slices.
     if (KIND == 0) {
@@ -446,6 +496,10 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
       if (!step(integral_constant<int, 3>{})) break;
     }
   }
+  STAMP(6);
+#ifdef MOE_EXP_STAMPS
+  if (PLAN && blockIdx.x < 64 && threadIdx.x == 0) ((uint64_t *)a.routed)[blockIdx.x * 16 + 7] = count;
+#endif
 }
 
 template <int KIND, int MT, int SPW, bool W4, bool FOLD = false, bool PLAN = false>

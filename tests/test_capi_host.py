@@ -77,7 +77,9 @@ def test_layout_for_qwen_shape():
     assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=193))
     assert lay.launches == 4
-    assert lay.partials % 256 == 0 and lay.act >= lay.partials + 13 * 129 * 4
+    assert lay.partials % 256 == 0 and lay.act >= lay.partials + 13 * 129 * 4 + 4
+    rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16 * 256))
+    assert lay.launches == 4
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16 * 256 + 1))
     assert lay.launches == 5  # more workgroups than CUs: separate router launch
     rc, lay = _layout(_desc(route=N.ROUTE_LOGITS, T=16))

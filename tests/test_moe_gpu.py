@@ -585,6 +585,35 @@ def test_gate_up_with_planning_prologue(tokens, gpu_device):
     assert plan.read_status() & 4
 
 
+@pytest.mark.parametrize("tokens,experts,k", [(17, 128, 8), (32, 128, 15), (16, 160, 8), (9, 256, 4),
+                                              (20, 128, 20), (24, 128, 21)])
+def test_w4_prologue_router_modes(tokens, experts, k, gpu_device):
+    """The W4 register-streaming gate/up routes in its prologue with 16 lanes
+    per token (E <= 128, K <= 16: up to 32 tokens in one pass), one full wave
+    per token, two tokens per wave interleaved (E > 128, T <= 16), or two
+    half-waves per wave (K > 16, T <= 32).  Each mode: IDs bit-exact with the
+    oracle's top-k on tie-heavy logits, weights to fp32 rounding, and the layer
+    within tolerance of the FP32 oracle on the dequantised weights."""
+    x, gu, dn, _, _ = O.make_inputs(tokens=tokens, experts=experts, topk=k, hidden=2048,
+                                    intermediate=256, id_dtype=torch.int32, pattern="random",
+                                    seed=tokens * experts + k)
+    packed = quantize_gate_up(gu)
+    tiled = tile_gate_up(packed).to(gpu_device)
+    g = torch.Generator().manual_seed(3 * tokens + k)
+    logits = torch.randint(-6, 6, (tokens, experts), generator=g).float() * 0.75
+    plan = prepare_routed_moe(*_to(gpu_device, x, logits), tiled, dn.to(gpu_device), k)
+    assert plan.launch_names == ("gate_up_swiglu", "down", "combine")
+    out = plan.forward()
+    torch.cuda.synchronize()
+    ids, w = O.route_topk(logits, k)
+    assert torch.equal(plan.ids.cpu(), ids), "router IDs differ"
+    assert torch.allclose(plan.routing_weights.cpu(), w, rtol=2e-6, atol=1e-7)
+    _check_dispatch(plan, ids, experts)
+    assert plan.read_status() == 0
+    m = O.error(out, O.moe_reference(x, O.dequantize_w4(packed.words, packed.scales), dn, ids, w))
+    assert m["passed"], m
+
+
 @pytest.mark.parametrize("tokens,decode", [(1, "exact"), (16, "exact"), (17, "exact"), (32, "exact"),
                                            (16, "fold"), (17, "fold"), (31, "fold")])
 def test_w4_gate_up_with_planning_prologue(tokens, decode, gpu_device):
