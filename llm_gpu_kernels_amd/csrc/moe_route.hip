@@ -375,6 +375,9 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
     else load_token_logits<false>(a.logits, rt, rt < t1, E, raw);
   }
   const uint32_t epoch = coherent_load(a.status + 2);
+  // status[1]: bits of a separate router launch earlier on this stream, read
+  // now so the last workgroup's final writes wait on no load.
+  const uint32_t router_bits = !ROUTER && tid == 0 ? a.status[1] : 0u;
   if (tid == 0) {
     s_flags = 0;
     s_all_flags = 0;
@@ -579,13 +582,12 @@ __global__ __launch_bounds__(kMultiThreads) void route_plan_multi_kernel(RouteAr
   }
   if (tid == 0 && (before & 0xffffu) == (uint32_t)W - 1u) {
     const bool any_bad = bad || (before >> 16) != 0;
-    // status[1]: bits of a separate router launch earlier on this stream.
-    uint32_t st = a.status[1] | (any_bad ? (all_flags & 7u) | kStatusStalled : all_flags);
+    uint32_t st = router_bits | (any_bad ? (all_flags & 7u) | kStatusStalled : all_flags);
     a.status[0] = st;
     a.status[1] = 0;
     *a.num_tasks = any_bad ? 0 : s_toff[E];
     coherent_store(arrive, 0u);
-    coherent_store(a.status + 2, coherent_load(a.status + 2) + 1u);
+    coherent_store(a.status + 2, epoch + 1u);  // every workgroup read this epoch
   }
 }
 

@@ -4,9 +4,12 @@
 // experts take ~1000 rows), streaming each weight byte once per 16/32-row task
 // would re-read the hot experts' weights dozens of times.  Here a task holds
 // up to BM = 64 grouped rows and a work unit is (task, n-tile of BN weight
-// rows); units are numbered n-tile-major so the consecutive tasks of one
-// expert share a weight tile, and consecutive units land on workgroups of the
-// same XCD, whose L2 then serves the repeated weight tile.
+// rows); units are numbered expert-major and n-tile-major within an expert,
+// and that sequence is cut into one contiguous chunk per XCD, so the tasks of
+// an expert that share a weight tile, and the n-tiles of a task that share its
+// token rows, are read through one XCD's L2 (HBM reads at T = 1024 Zipf:
+// gate/up 765 -> 661 MB, down 382 -> 312 MB, against 4-task blocks dealt
+// round-robin).
 //
 // Per unit: a K loop over BK-wide stages.  Each stage's weight tile [BN][BK]
 // and token tile [BM][BK] go global -> LDS (the warp-specialised kernel
@@ -47,10 +50,6 @@ __device__ __forceinline__ int swz(int row, int c) {
   else return row * 256 + ((c ^ (row & 15)) << 4);
 }
 
-#ifndef MOE_TILE_TASK_BLOCK
-#define MOE_TILE_TASK_BLOCK 4
-#endif
-constexpr int kTaskBlock = MOE_TILE_TASK_BLOCK;
 
 template <int KIND>
 struct TileCfg {
@@ -103,23 +102,37 @@ __global__ __launch_bounds__(kWsThreads) void tile_ws_kernel(ExpertArgs a) {
   const int total = num_tasks * ntiles;
   const MOE_CONST int32_t *tasks = as_const((const int32_t *)a.tasks);
   const int G = gridDim.x;
-  const int slot = (G % 8) ? (int)blockIdx.x : (int)(blockIdx.x / 8 + (blockIdx.x % 8) * (G / 8));
-  const int nu = slot < total ? (total - slot + G - 1) / G : 0;
+  // XCD-affine order: the unit sequence, expert-major and n-tile-major
+  // within an expert (every task of the expert on one n-tile, then the next
+  // n-tile), is cut into eight contiguous chunks, one per XCD (consecutive
+  // workgroup IDs go round-robin over the XCDs), and the workgroups of an XCD
+  // walk their chunk together.  So an expert's weight tile and its tasks'
+  // token rows are read from one XCD's L2, except at the seven chunk edges.
+  const bool xcd_mode = G % 8 == 0 && G >= 8;
+  const int P = xcd_mode ? G / 8 : G;            // workgroups per XCD
+  const int xcd = xcd_mode ? (int)blockIdx.x % 8 : 0;
+  const int p = xcd_mode ? (int)blockIdx.x / 8 : (int)blockIdx.x;
+  const int CH = xcd_mode ? (total + 7) / 8 : total;  // units per chunk
+  const int c_end = min(CH, total - xcd * CH);
+  const int nu = p < c_end ? (c_end - p + P - 1) / P : 0;
+  const MOE_CONST int32_t *cnts = as_const(a.counts);
+  const MOE_CONST int32_t *offs = as_const(a.offsets);
   const int nstages = nu * KT;
 
-  // Unit i of this workgroup: blocks of kTaskBlock tasks, n-tile-major within a block.
   struct Unit {
     int e, row0, rows, nt;
   };
   auto unit_of = [&](int i) {
-    const int u = slot + i * G;
-    const int blk = u / (kTaskBlock * ntiles);
-    const int rem = u - blk * (kTaskBlock * ntiles);
-    const int mb = min(kTaskBlock, num_tasks - blk * kTaskBlock);
+    const int L = xcd * CH + p + i * P;
+    const int T = L / ntiles;  // the task whose expert owns unit L
+    const int e = tasks[4 * T];
+    const int t0 = T - (tasks[4 * T + 1] - offs[e]) / BM;  // the expert's first task
+    const int m = (cnts[e] + BM - 1) / BM;                 // and its task count
+    const int local = L - ntiles * t0;
     Unit un;
-    un.nt = rem / mb;
-    const int t = blk * kTaskBlock + (rem - un.nt * mb);
-    un.e = tasks[4 * t];
+    un.nt = local / m;
+    const int t = t0 + (local - un.nt * m);
+    un.e = e;
     un.row0 = tasks[4 * t + 1];
     un.rows = tasks[4 * t + 2];
     return un;
