@@ -267,6 +267,15 @@ struct SmallPlanOut {
   uint32_t *status;
 };
 
+// Workgroup barrier ordering LDS only.  __syncthreads() is also a release
+// fence for global memory, which waits for every load the workgroup has in
+// flight -- the streaming gate/up requests its first weights before planning.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Bits of an expert id below E (E <= 256).
 __device__ __forceinline__ int id_bits(int E) { return E <= 1 ? 1 : 32 - __builtin_clz((unsigned)(E - 1)); }
 
@@ -296,7 +305,7 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
   }
   const int lrank = __popcll(match & lanemask_lt());
   if (ok && lrank == 0) s.wcnt[wave * E + id] = __popcll(match);
-  __syncthreads();
+  lds_sync();
   if (wave == 0) {
     // Per expert (four per lane): counts of the waves holding routes ->
     // exclusive prefixes in place, then exclusive scans of the counts and
@@ -340,7 +349,7 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
       *s.ntasks = trun;
     }
   }
-  __syncthreads();
+  lds_sync();
   const int valid_rows = s.off[E - 1] + s.cnt[E - 1];
   if (ok) {
     const int rank = s.wcnt[wave * E + id] + lrank;
@@ -373,7 +382,7 @@ __device__ inline void plan_small(const SmallPlanLds &s, const SmallPlanOut &go,
     }
   }
   if (flags) atomicOr(s.flags, flags);
-  __syncthreads();
+  lds_sync();
   if (g && tid == 0) {
     *g->num_tasks = s.toff[E];
     // Write-through: a later workgroup of the same launch may OR a bit into
