@@ -81,15 +81,6 @@ constexpr size_t stream_lds(bool plan) {
          (FOLD ? (size_t)kWaves * (SPW / 4) * MT * 16 * sizeof(float) : 0) + (plan ? kPlanLds : 0);
 }
 
-#ifdef MOE_EXP_STAMPS
-#define STAMP(k)                                                                              \
-  do {                                                                                        \
-    if (PLAN && blockIdx.x < 64 && threadIdx.x == 0)                                          \
-      ((uint64_t *)a.routed)[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime();      \
-  } while (0)
-#else
-#define STAMP(k) do {} while (0)
-#endif
 template <int KIND, int MT, int SPW, bool W4, bool FOLD, bool PLAN = false>
 __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertArgs a, RouteArgs ra) {
   constexpr int NRB = 2;
@@ -106,7 +97,6 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
   const int4 *l_tasks = nullptr;
   const int *l_row = nullptr;
   int ntasks = 0;
-  STAMP(0);
   if constexpr (PLAN) {
     using namespace route_dev;
     uint8_t *pl = (uint8_t *)s_red + stream_lds<KIND, MT, SPW, W4, FOLD>(false);
@@ -147,10 +137,6 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
     }
     for (int i = tid; i < kWaves * ra.E; i += kThreads) x_wcnt[i] = 0;
     if (tid == 0) *x_flags = 0;
-#ifdef MOE_EXP_STAMPS
-    __builtin_amdgcn_s_waitcnt(0);
-    STAMP(4);
-#endif
     const bool g0 = blockIdx.x == 0;
     if (g0 && tid < 4) ra.counters[tid] = 0;
     uint32_t flags = 0;
@@ -175,13 +161,11 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
       }
     }
     __syncthreads();
-    STAMP(1);
     const SmallPlanLds L{x_ids, x_w, x_wcnt, x_cnt, x_off, x_toff, p_tasks, p_row, p_nt, x_flags};
     const SmallPlanOut O{ra.counts, ra.offsets, ra.ranks, ra.map, ra.row_route, ra.row_token,
                          ra.tasks, ra.num_tasks, ra.status};
     plan_small<kThreads>(L, O, g0, ra.R, ra.E, ra.K, 16, flags);
     ntasks = *p_nt;
-    STAMP(2);
     l_tasks = p_tasks;
     l_row = p_row;
   }
@@ -303,11 +287,7 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
         const size_t rbi = (size_t)ex * (2 * I / 16) + cb + (rb ? I / 16 : 0);
 #pragma unroll
         for (int i = 0; i < AW; ++i) {
-#ifdef MOE_EXP_NOLOAD
-          const size_t unit = (size_t)((s0 >> 2) + i) + (rb ? G4 : 0) + 0 * rbi;
-#else
           const size_t unit = rbi * G4 + (s0 >> 2) + i;
-#endif
           buf[rb][i] = ((const u32x4 *)a.w4_words)[unit * kWave + lane];
           sc[rb][i] = a.w4_scales[unit * 16 + r];
         }
@@ -338,7 +318,6 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
     }
   }
   int btask = mq[0].task;
-  STAMP(3);
 
   int i = 0;
   int parity = 0;
@@ -386,13 +365,7 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
           const W4Scale ks = w4_scale(bf16_bits_to_f32(sq[SL][rb][i]));
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-#ifdef MOE_EXP_NODECODE
-            const uint32_t wq = aq[SL][rb][i][j];
-            const u32x4 af = u32x4{wq, wq, wq, wq};
-            (void)ks;
-#else
             const u32x4 af = w4_decode8(aq[SL][rb][i][j], ks);
-#endif
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = mfma16(af, bfr[mt][i * 4 + j], acc[rb][mt]);
           }
@@ -425,9 +398,7 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
         }
       }
 
-#ifndef MOE_EXP_NOBARRIER
     lds_barrier();
-#endif
 
     // Epilogue of cur: fixed-order sum of the eight K-slices.
     if (KIND == 0) {
@@ -496,10 +467,6 @@ __global__ __launch_bounds__(kThreads, FOLD ? 4 : 1) void stream_kernel(ExpertAr
       if (!step(integral_constant<int, 3>{})) break;
     }
   }
-  STAMP(6);
-#ifdef MOE_EXP_STAMPS
-  if (PLAN && blockIdx.x < 64 && threadIdx.x == 0) ((uint64_t *)a.routed)[blockIdx.x * 16 + 7] = count;
-#endif
 }
 
 template <int KIND, int MT, int SPW, bool W4, bool FOLD = false, bool PLAN = false>
