@@ -92,6 +92,11 @@ constexpr int kSeqRing = 8;
 // measured 2-8 us faster per launch than single units at T = 17 and 193, and
 // than larger blocks, which leave longer tails; the 32-row units of down
 // with 32-row tasks go in fours (T = 300-480: down 3-7 us faster than pairs).
+// The last G counter-served units go out one per step: a pair taken at the
+// very end held its workgroup ~8 us (two 128 KiB units) past the others
+// (per-workgroup stamps at BF16 T = 17: median end 86 us, last 92.7 us).
+// With PLAN (routing in the prologue) the first unit of workgroup b is named
+// before routing (see the kernel) and its stages load during the prologue.
 template <int KIND, int MT>
 constexpr int kChunkOf = KIND == 1 && MT == 2 ? 4 : 2;
 
@@ -178,16 +183,65 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   const int4 *l_tasks = nullptr;
   const int *l_row_token = nullptr;
   int ntasks = 0;
+  const int G = gridDim.x;
+  int32_t *const wcnt = a.counters + 2 * KIND;
+  int *const seq = (int *)(smem + NS * C::STAGE + C::RED);
+  // PLAN: speculative first unit.  Workgroup b < C0 E (C0 = G / E column
+  // blocks per expert) starts with column block b / E of expert b % E, which
+  // it can name before routing.  Its loader waves that route no token stream
+  // that unit's first NS - 1 stages into the stage ring while the workgroup
+  // routes and plans (HBM is otherwise idle then).  After planning the unit
+  // is kept when the expert is active and has a single task (then the units
+  // with column block < C0 of every task are exactly the workgroups' first
+  // units), and the prefetched stages are discarded otherwise.  Every other
+  // unit comes from the counter.
+  constexpr int kPrefetch = NS - 1 < SPU ? NS - 1 : SPU;  // stages of unit 0 prefetched
+  int spec_u = -1;      // the kept speculative unit (PLAN)
+  bool spec_pf = false; // this wave issued prefetch loads (PLAN loaders)
+  int nsc = 0;          // column blocks per task taken by first units (PLAN)
+  int c_first = 0;      // wave 0, lane 0: the first counter chunk (PLAN)
   if constexpr (PLAN) {
     using namespace route_dev;
     uint8_t *pa = smem + NS * C::STAGE + C::RED + C::SEQB;
     int4 *p_tasks = (int4 *)pa;
     int *p_row = (int *)(pa + kPlanTaskMax * 16);
     int *p_nt = p_row + kSmallPlanRoutes + 64;
-    // Scratch in the (still idle) stage ring.
-    int *x_ids = (int *)smem;
-    float *x_w = (float *)(smem + 4 * kSmallPlanRoutes);
-    int *x_wcnt = (int *)(smem + 8 * kSmallPlanRoutes);
+    const int E = ra.E;
+    const int C0 = min(G / E, ncb);
+    const bool spec_wg = (int)blockIdx.x < C0 * E;
+    const int se = (int)blockIdx.x % E, scb = (int)blockIdx.x / E;
+    const bool half = ra.fuse_router == 2;
+    const int nroute = min(kConsumers + kLoaders, half ? (ra.T + 1) / 2 : ra.T);  // routing waves
+    const int free0 = max(kConsumers, nroute);  // loader waves >= free0 route no token
+    if (spec_wg && wave >= free0) {
+      // Stage s, piece p (stage row p * RPI + lane / LPR, 16-byte chunk
+      // lane % LPR, XOR-swizzled as the loaders place it), the free loader
+      // waves' pieces in turn.
+      constexpr int RPI = 1024 / (KC * 2), LPR = kWave / RPI, NP = C::STAGE / 1024;
+      const int nfree = kConsumers + kLoaders - free0, fi = wave - free0;
+      const int lrow = lane / LPR, lch = lane % LPR;
+      for (int q = fi; q < kPrefetch * NP; q += nfree) {
+        const int st = q / NP, pc = q - st * NP;
+        const int R = pc * RPI + lrow;
+        const size_t grow = (size_t)se * 2 * I + (R < 16 ? scb * 16 + R : I + scb * 16 + R - 16);
+        const uint16_t *src = a.gate_up + grow * K + (lch ^ (R & 15)) * 8 + st * KC;
+        __builtin_amdgcn_global_load_lds((const void *)src,
+                                         (__attribute__((address_space(3))) void *)(smem + st * C::STAGE + pc * 1024),
+                                         16, 0, 0);
+      }
+      spec_pf = true;
+    }
+    // The first counter chunk: requested by the last wave (which routes a
+    // token only from T = 31 on) after its prefetch loads, used after
+    // planning; it passes through the last unit-ring slot.
+    if (wave == kConsumers + kLoaders - 1 && lane == 0) seq[kSeqRing - 1] = atomicAdd(wcnt, 1);
+    // Scratch in the last stage buffer (the prefetch fills the others).
+    uint8_t *scr = smem + (NS - 1) * C::STAGE;
+    static_assert(12 * kSmallPlanRoutes + 4 * kSmallPlanWaves * kMaxExperts + 12 * kMaxExperts + 8 <= C::STAGE,
+                  "planning scratch fits one stage");
+    int *x_ids = (int *)scr;
+    float *x_w = (float *)(scr + 4 * kSmallPlanRoutes);
+    int *x_wcnt = (int *)(scr + 8 * kSmallPlanRoutes);
     int *x_cnt = x_wcnt + kSmallPlanWaves * kMaxExperts;
     int *x_off = x_cnt + kMaxExperts;
     int *x_toff = x_off + kMaxExperts;
@@ -195,12 +249,13 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     // One token per wave (fuse_router 1) or half-wave (2); logits first.
     // (16 lanes per token measured 0.4 us slower here: the sixteen waves
     // route up to 32 tokens in one pass either way.)
-    const bool half = ra.fuse_router == 2;
     const int ft = half ? 2 * wave + (lane >> 5) : wave;
     const bool fwave = half ? 2 * wave < ra.T : wave < ra.T;  // wave-uniform
     float raw[4];
-    if (half) load_token_logits<true>(ra.logits, ft, ft < ra.T, ra.E, raw);
-    else load_token_logits<false>(ra.logits, ft, ft < ra.T, ra.E, raw);
+    if (fwave) {  // waves that route no token skip the loads (and their waits)
+      if (half) load_token_logits<true>(ra.logits, ft, ft < ra.T, ra.E, raw);
+      else load_token_logits<false>(ra.logits, ft, ft < ra.T, ra.E, raw);
+    }
     for (int i = tid; i < kSmallPlanWaves * ra.E; i += kThreads) x_wcnt[i] = 0;
     if (tid == 0) *x_flags = 0;
     const bool g0 = blockIdx.x == 0;
@@ -213,7 +268,9 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
       else
         route_token<false>(raw, ft, true, ra.E, ra.K, ra.renormalize, ids_g, w_g, flags, x_ids, x_w);
     }
-    __syncthreads();
+    // LDS-only barrier: a full one would make the prefetching waves wait for
+    // their stage loads.
+    lds_sync();
     const SmallPlanLds L{x_ids, x_w, x_wcnt, x_cnt, x_off, x_toff, p_tasks, p_row, p_nt, x_flags};
     const SmallPlanOut O{ra.counts, ra.offsets, ra.ranks, ra.map, ra.row_route, ra.row_token,
                          ra.tasks, ra.num_tasks, ra.status};
@@ -221,22 +278,78 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     ntasks = *p_nt;
     l_tasks = p_tasks;
     l_row_token = p_row;
+    // First units are kept when every active expert has one task (always
+    // below 17 tokens): then the counter hands out column blocks >= C0.
+    bool one_task = true;
+    for (int e = lane; e < E; e += kWave) one_task &= x_cnt[e] <= 16;
+    one_task = __builtin_amdgcn_readfirstlane((int)(__ballot(!one_task) == 0)) != 0;
+    nsc = one_task && C0 > 0 ? C0 : 0;
+    if (nsc > 0 && spec_wg && x_cnt[se] > 0) spec_u = x_toff[se] * ncb + scb;
   }
   // The planning gate/up launch is the first of its forward: it zeroes the
   // down launch's counters (which start only after this launch ends).
   if (PLAN && blockIdx.x == 0 && tid < 2) a.counters[2 + tid] = 0;
   const int total = (PLAN ? ntasks : *as_const(a.num_tasks)) * ncb;
-  const int G = gridDim.x;
   constexpr int A = kAheadOf<NS, SPU>;
   static_assert(A + 1 <= kSeqRing, "unit ring");
-  int32_t *const wcnt = a.counters + 2 * KIND;
-  int *const seq = (int *)(smem + NS * C::STAGE + C::RED);
-  // Units taken without the counter: S consecutive ones per workgroup.
-  // (Static shares up to 7/8 of the work, the rest from the counter,
-  // measured slower: the per-workgroup streaming rate varies too much.)
-  constexpr int S = A;
+  constexpr int CH = kChunkOf<KIND, MT>;
+  // Units taken without the counter.  Without PLAN: S consecutive ones per
+  // workgroup (static shares up to 7/8 of the work, the rest from the
+  // counter, measured slower: the per-workgroup streaming rate varies too
+  // much).  With PLAN: the kept first unit, then the counter from the start
+  // (MFMA wave 0 takes the first A units after planning and publishes them in
+  // the unit ring).
+  constexpr int S = PLAN ? 0 : A;
   const int ub = (int)blockIdx.x * S;  // this workgroup's first unit
-  if (ub >= total) {
+  // Counter-served units: value v -> unit v + S G, or with PLAN (task
+  // v / (ncb - nsc), column block nsc + v % (ncb - nsc)); total_v in all.
+  const int ncv = ncb - nsc;
+  const int total_v = PLAN ? ntasks * ncv : max(0, total - S * G);
+  auto unit_of_v = [&](int v) -> int {
+    if (v < 0 || v >= total_v) return total;
+    if (!PLAN) return v + S * G;
+    const int t = v / ncv;
+    return t * ncb + nsc + (v - t * ncv);
+  };
+  // Counter value c hands out CH consecutive values while c < cs, then one
+  // value each: the last round of units goes out singly, so that no
+  // workgroup takes a long chunk at the very end (the launch's tail).
+  const int cs = max(0, (total_v - G) / CH);
+  auto chunk_of = [&](int c, int &base, int &size) {
+    if (c < cs) {
+      base = CH * c;
+      size = CH;
+    } else {
+      base = CH * cs + (c - cs);
+      size = 1;
+    }
+  };
+  // Wave 0, lane 0: the counter walk -- value of the unit taken last, the
+  // current chunk (base, size; size < 0 while its add is in flight in
+  // `cpend`) and the values of it used.
+  int taken = 0, tbase = 0, tsize = 0, tpos = 0, cpend = 0;
+  if constexpr (PLAN) {
+    if (wave == 0 && lane == 0) {
+      c_first = seq[kSeqRing - 1];
+      chunk_of(c_first, tbase, tsize);
+      int k = 0;
+      if (spec_u >= 0) seq[k++] = spec_u;
+      for (; k < A; ++k) {
+        if (tpos == tsize) {
+          chunk_of(atomicAdd(wcnt, 1), tbase, tsize);
+          tpos = 0;
+        }
+        taken = tbase + tpos++;
+        seq[k] = unit_of_v(taken);
+      }
+    }
+    __syncthreads();
+    if (seq[0] >= total) {
+      if (spec_pf) wait_vmcnt<0>();
+      if (tid == 0) finish_units(wcnt, G, 0, total, a.status);
+      return;
+    }
+  } else if (ub >= total) {
     if (tid == 0) finish_units(wcnt, G, 0, total, a.status);
     return;
   }
@@ -282,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
     // Unit k of this workgroup (k >= A: published by MFMA wave 0, read
     // through an instruction the compiler cannot see).
     auto unit_at = [&](int k) -> int {
-      if (k < S) return ub + k;
+      if (!PLAN && k < S) return ub + k;
       uint32_t v;
       asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
                    : "=v"(v)
@@ -313,6 +426,16 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
             (__attribute__((address_space(3))) void *)(buf + (lw * PER + j) * 1024), 16, 0, 0);
       ++issued;
     };
+    if (PLAN && spec_pf) {
+      // The prefetched stages have landed (issued before routing); they are
+      // unit 0's first kPrefetch stages when the speculative unit was kept.
+      wait_vmcnt<0>();
+      if (spec_u >= 0) {
+        setup(spec_u, expert_of(spec_u / ncb));
+        cur = 0;
+        issued = kPrefetch;
+      }
+    }
     while (issued < NS - 1 && !ended) issue();
     for (int st = 0; st < issued; ++st) {
       // Stage st has landed once at most the loads issued after it remain.
@@ -430,10 +553,9 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
   // Unit k of this workgroup, k >= A: published by MFMA wave 0 at the start
   // of unit k - A + 1 (visible to every wave one barrier later).
   auto unit_at = [&](int k) -> int { return k < S ? ub + k : seq[k % kSeqRing]; };
-  Meta prev, cur = meta_of(ub), next;
+  Meta prev, cur = meta_of(unit_at(0)), next;
   load_b(cur, bfr);
   int done_units = 0;  // units this workgroup ran (known when its loop ends)
-  int taken = 0;       // wave 0, lane 0: counter value of the unit taken last
   bool taking = true;  // wave 0: the units taken so far are all in range
   bool pending = false;
   int st = 0;
@@ -451,14 +573,25 @@ __global__ __launch_bounds__(kThreads) void dma_kernel(ExpertArgs a, RouteArgs r
         if (i > 0) epilogue(prev, (i - 1) % C::PAR, (i - 1) & 1);
         if (wave == 0) {
           if (pending) {  // unit i - 1 + A, taken at the start of unit i - 1
-            int u = __builtin_amdgcn_readfirstlane(taken) + S * G;
-            if (u < 0) u = total;  // a corrupted counter ends the workgroup's units
+            if (lane == 0 && tsize < 0) {  // a new chunk: its add has returned by now
+              chunk_of(cpend, tbase, tsize);
+              taken = tbase;
+              tpos = 1;
+            }
+            const int u = unit_of_v(__builtin_amdgcn_readfirstlane(taken));
             if (lane == 0) seq[(i - 1 + A) % kSeqRing] = u;
-            taking = u < total;
+            taking = u < total;  // (a corrupted counter ends the workgroup's units)
             pending = false;
           }
           if (taking) {  // unit i + A
-            if (lane == 0) taken = (i % kChunkOf<KIND, MT>) ? taken + 1 : kChunkOf<KIND, MT> * atomicAdd(wcnt, 1);
+            if (lane == 0) {
+              if (tsize > 0 && tpos < tsize) {
+                taken = tbase + tpos++;
+              } else {
+                cpend = atomicAdd(wcnt, 1);
+                tsize = -1;
+              }
+            }
             pending = true;
           }
         }
