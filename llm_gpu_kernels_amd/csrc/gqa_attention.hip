@@ -10,20 +10,20 @@
 //   reference does), the output is bf16.
 //
 // Design.  A workgroup of four or eight waves owns 16 * RB query rows of one
-// KV head (RB = 2: two 16-row blocks, each one query head x 16 tokens).  The
+// KV head (RB = 1 or 2 16-row blocks, each one query head x 16 tokens).  The
 // waves split the workgroup's visible keys into contiguous ranges and each
 // wave runs its own online softmax over all of the workgroup's rows, 32 keys
 // per step, with no workgroup barrier in the loop:
 //   * scores are computed transposed, S^T = K Q^T, with 16x16x32 bf16 MFMAs;
-//     K fragments (A operand) are loaded from HBM straight into registers,
 //     Q fragments (B operand) stay in registers for the whole kernel, and the
 //     score tile lands in the A-operand layout of the P.V MFMA, so P never
 //     goes through LDS;
-//   * V rows are staged row-major (16-byte XOR swizzle) in a wave-private LDS
-//     area and read back with ds_read_b64_tr_b16, whose 16-lane transpose
-//     yields the B operand (8 keys x 1 dim per lane) directly;
-//   * the next step's K and V are prefetched into registers while the current
-//     step computes.
+//   * each step's K and V rows go from HBM straight into a wave-private K
+//     stage and V stage in LDS (buffer loads with an LDS destination, whole
+//     128-byte lines per load); K is read back as A fragments, V with
+//     ds_read_b64_tr_b16, whose 16-lane transpose yields the B operand
+//     directly; the next step's loads are issued while the current one
+//     computes.
 // At the end the waves' (max, sum, O) states are merged in LDS in fixed wave
 // order.  When there are too few workgroups to fill the chip the keys are
 // also split across workgroups and a second kernel merges the partial states
@@ -40,9 +40,6 @@ namespace {
 constexpr int kD = 128;      // head_dim
 constexpr int kKC = 32;      // keys per wave step
 constexpr int kMaxSplits = 16;
-#ifndef GQA_ROW_BLOCKS
-#define GQA_ROW_BLOCKS 2
-#endif
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -597,65 +594,74 @@ __global__ __launch_bounds__(128) void gqa_merge_kernel(GqaArgs a, int nsplit) {
 
 }  // namespace
 
-// Row blocks per wave and query heads per workgroup of the launched variant.
-constexpr int kLaunchRB = GQA_ROW_BLOCKS;
-int gqa_heads_per_wg(int G) { return G < kLaunchRB ? G : kLaunchRB; }
+// Query heads per workgroup: RB row blocks of one head each, as many heads as
+// the group has.
+int gqa_heads_per_wg(int G, int rb) { return G < rb ? G : rb; }
 
-// Workgroups (of either width) cover 16 * RB query rows each.  With enough of
-// them for two per CU: four-wave workgroups, no split.  Otherwise eight-wave
-// workgroups, one per CU (the same two waves per SIMD, keys split eight ways
-// inside the workgroup and merged in LDS), and the keys are split across
-// workgroups half as many times as would fill the CUs: the merge launch and
-// its partial states cost more than the idle CUs (on 256 CUs, T = 32: four
-// splits 14.2 us, eight 15.2, two 15.5, none 16.8; T = 96: none 17.8 us, two
-// 18.3).  With one workgroup per CU or more there is no merge launch at all.
+int gqa_workgroups(int T, int Hkv, int G, int rb) {
+  const int hpw = gqa_heads_per_wg(G, rb), qt = 16 * (rb / hpw);
+  return ((T + qt - 1) / qt) * Hkv * (G / hpw);
+}
+
+// Launch shape.  While workgroups of one 16-row block per wave (RB = 1) fit
+// the CUs once, those: the per-step chain of each wave is half as long and
+// twice as many CUs work.  Eight-wave workgroups when they fill more than half
+// the CUs, else four-wave ones with the keys split across up to four
+// workgroups (256 CUs, config-5 heads: T = 16 / 32 / 48 / 64 / 96 / 128 take
+// 10.4 / 11.4 / 14.0 / 14.6 / 15.4 / 15.7 us against 13.7 / 14.1 / 16.0 /
+// 16.3 / 16.8 / 17.1 us with RB = 2).  Beyond that two row blocks per wave
+// (RB = 2, each K/V step shared by 32 rows): with enough workgroups for two
+// per CU, four-wave workgroups and no split; otherwise eight-wave
+// workgroups, one per CU, and the keys split half as many times as would fill
+// the CUs (the merge launch and its partial states cost more than idle CUs).
 GqaShape gqa_shape(int T, int Hq, int Hkv, int num_cus) {
-  const int G = Hq / Hkv, hpw = gqa_heads_per_wg(G);
-  const int qt = 16 * (kLaunchRB / hpw);
-  const int wgs = ((T + qt - 1) / qt) * Hkv * (G / hpw);
-  if (wgs <= 0) return {1, 4};
-  const int per_cu = 4 / kLaunchRB;  // resident four-wave workgroups per CU
-  if (wgs >= num_cus * per_cu) return {1, 4};
-  const int waves = kLaunchRB == 2 ? 8 : 4;
-  const int slots = waves == 8 ? num_cus : num_cus * per_cu;
-  int s = slots / wgs / 2;
+  const int G = Hq / Hkv;
+  const int w1 = gqa_workgroups(T, Hkv, G, 1);
+  if (w1 <= 0) return {1, 4, 2};
+  if (w1 <= num_cus) {
+    if (2 * w1 > num_cus) return {1, 8, 1};
+    const int s = num_cus / w1;
+    return {s < 4 ? s : 4, 4, 1};
+  }
+  const int w2 = gqa_workgroups(T, Hkv, G, 2);
+  if (w2 >= 2 * num_cus) return {1, 4, 2};
+  int s = num_cus / w2 / 2;
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
-  return {s, waves};
+  return {s, 8, 2};
 }
 
 size_t gqa_partial_bytes(int T, int Hq, int nsplit) {
   return nsplit > 1 ? (size_t)nsplit * T * Hq * (kD + 2) * sizeof(float) : 0;
 }
 
-template <int NW>
+template <int RB, int NW>
 hipError_t launch_fwd(const GqaArgs &a, int hpw, dim3 grid, int groups, int nqb, int nsplit,
                       hipStream_t s) {
   const dim3 block(64 * NW);
-  switch (hpw) {
-    case 1: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 1, NW>), grid, block, 0, s, a, groups, nqb, nsplit); break;
-    case 2: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 2, NW>), grid, block, 0, s, a, groups, nqb, nsplit); break;
-#if GQA_ROW_BLOCKS == 4
-    case 4: hipLaunchKernelGGL((gqa_fwd_kernel<kLaunchRB, 4, NW>), grid, block, 0, s, a, groups, nqb, nsplit); break;
-#endif
-    default: return hipErrorInvalidValue;
-  }
+  if (hpw == 1)
+    hipLaunchKernelGGL((gqa_fwd_kernel<RB, 1, NW>), grid, block, 0, s, a, groups, nqb, nsplit);
+  else if (RB == 2 && hpw == 2)
+    hipLaunchKernelGGL((gqa_fwd_kernel<2, 2, NW>), grid, block, 0, s, a, groups, nqb, nsplit);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 hipError_t launch_gqa(const GqaArgs &a, GqaShape shape, hipStream_t s) {
   if (a.T == 0) return hipSuccess;
-  const int G = a.Hq / a.Hkv, hpw = gqa_heads_per_wg(G);
-  const int qt = 16 * (kLaunchRB / hpw), groups = G / hpw;
+  const int rb = shape.rb, G = a.Hq / a.Hkv, hpw = gqa_heads_per_wg(G, rb);
+  const int qt = 16 * (rb / hpw), groups = G / hpw;
   const int nqb = (a.T + qt - 1) / qt;
   const int nsplit = shape.nsplit;
   const dim3 grid(nqb * a.Hkv * groups * nsplit);
   hipError_t e;
-#if GQA_ROW_BLOCKS == 2
-  if (shape.waves == 8) e = launch_fwd<8>(a, hpw, grid, groups, nqb, nsplit, s);
+  if (rb == 1)
+    e = shape.waves == 8 ? launch_fwd<1, 8>(a, hpw, grid, groups, nqb, nsplit, s)
+                         : launch_fwd<1, 4>(a, hpw, grid, groups, nqb, nsplit, s);
   else
-#endif
-    e = launch_fwd<4>(a, hpw, grid, groups, nqb, nsplit, s);
+    e = shape.waves == 8 ? launch_fwd<2, 8>(a, hpw, grid, groups, nqb, nsplit, s)
+                         : launch_fwd<2, 4>(a, hpw, grid, groups, nqb, nsplit, s);
   if (e != hipSuccess || nsplit == 1) return e;
   hipLaunchKernelGGL(gqa_merge_kernel, dim3(a.T * a.Hq), dim3(kD), 0, s, a, nsplit);
   return hipGetLastError();

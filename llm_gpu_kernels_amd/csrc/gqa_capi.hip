@@ -79,7 +79,7 @@ extern "C" {
 
 int gqa_seg_workspace_bytes(const gqa_seg_desc *d, size_t *bytes) {
   int dev = 0, cus = 0;
-  moe::GqaShape shape{1, 4};
+  moe::GqaShape shape{1, 4, 2};
   int rc = device_cus(&dev, &cus);
   if (rc) return rc;
   if ((rc = validate(d, cus, &shape))) return rc;
@@ -92,7 +92,7 @@ int gqa_seg_plan_create(gqa_seg_plan **out, const gqa_seg_desc *d) {
   if (!out) return moe::capi_fail(MOE_EINVAL, "null plan pointer");
   *out = nullptr;
   int dev = 0, cus = 0;
-  moe::GqaShape shape{1, 4};
+  moe::GqaShape shape{1, 4, 2};
   int rc = device_cus(&dev, &cus);
   if (rc) return rc;
   if ((rc = validate(d, cus, &shape))) return rc;

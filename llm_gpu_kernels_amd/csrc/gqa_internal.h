@@ -23,10 +23,11 @@ struct GqaArgs {
 };
 
 // Launch shape: key splits across workgroups (merged by a second kernel when
-// > 1) and waves per workgroup (4 or 8).
+// > 1), waves per workgroup (4 or 8) and 16-row blocks per wave (1 or 2).
 struct GqaShape {
   int nsplit;
   int waves;
+  int rb;
 };
 GqaShape gqa_shape(int T, int Hq, int Hkv, int num_cus);
 size_t gqa_partial_bytes(int T, int Hq, int nsplit);

@@ -45,12 +45,16 @@ def test_baseline_config5(tokens, gpu_device):
     _check(plan.output, q, segs)
 
 
-@pytest.mark.parametrize("tokens", [200, 512])
-def test_launch_shapes(tokens, gpu_device):
-    """The other launch shapes on 256 CUs: T = 200 runs eight-wave workgroups
-    without a split (fewer workgroups than CUs, no merge launch); T = 512 runs
-    four-wave workgroups, two per CU, without a split."""
-    q, segs = _values(tokens + 1, tokens, (300, 0, 129), gpu_device)
+@pytest.mark.parametrize("tokens,hq,hkv", [(40, 32, 8), (100, 32, 8), (200, 32, 8), (512, 32, 8),
+                                           (600, 8, 8)])
+def test_launch_shapes(tokens, hq, hkv, gpu_device):
+    """Every launch shape on 256 CUs (gqa_shape).  One 16-row block per wave:
+    T = 40 four-wave workgroups with the keys split in two (merge launch),
+    T = 100 eight-wave workgroups without a split.  Two row blocks per wave:
+    T = 200 eight-wave workgroups without a split, T = 512 four-wave
+    workgroups, two per CU; T = 600 with one query head per KV head (two
+    token blocks per workgroup)."""
+    q, segs = _values(tokens + 1, tokens, (300, 0, 129), gpu_device, hq=hq, hkv=hkv)
     plan = prepare_segmented_gqa(q, segs)
     torch.cuda.synchronize()
     _check(plan.output, q, segs)
