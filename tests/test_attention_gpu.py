@@ -77,6 +77,16 @@ def test_group_sizes(hq, hkv, gpu_device):
     _check(plan.output, q, segs)
 
 
+def test_split_merge_partial_workgroup(gpu_device):
+    """T * Hq = 66 (query) rows with the keys split: the merge launch's last
+    workgroup holds fewer rows than the others."""
+    q, segs = _values(5, 33, (200, 17, 0), gpu_device, hq=2, hkv=1)
+    plan = prepare_segmented_gqa(q, segs)
+    torch.cuda.synchronize()
+    assert plan.splits_workspace_bytes > 0
+    _check(plan.output, q, segs)
+
+
 def test_empty_query(gpu_device):
     q, segs = _values(1, 0, (10, 0, 4), gpu_device)
     plan = prepare_segmented_gqa(q, segs)
